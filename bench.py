@@ -1,0 +1,278 @@
+"""Benchmark of the paged KV-cache path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu-baseline]
+
+A step is one paged-decode pass over the Qwen3-0.6B decode workload (256 sequences,
+16 query / 8 kv heads, head_dim 128, bf16, context lengths uniform over 100-2048,
+256-token blocks drawn from a shuffled 4096-block pool), with every input resident in
+HBM.  `value` is algorithmic HBM bytes per step / time per step (GB/s), timed with HIP
+events on the launch stream over exactly K steps after W warm-up steps.
+
+The same run also reports, as extra fields (not the headline): the KV append (4096
+tokens x 8 heads x 128 into a [512, 256, 8, 128] cache, 128 padding slots), the
+Qwen3-8B decode workload (128 sequences, 32/8 heads, contexts 1024-32768, 20000-block
+pool) and the prefix-cached varlen prefill (32 sequences, 100-1024 new tokens, prefixes
+of 0-4096 tokens shared by groups of 4).  `cpu_baseline` times the PyTorch-eager CPU
+restatement (gather + SDPA in bf16) on a bounded sample of the headline workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "paged-decode HBM GB/s (% of 8 TB/s) + KV-append GB/s; Qwen3-0.6B e2e tok/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+BS, D = 256, 128
+SCALE = D ** -0.5
+
+
+# ----------------------------------------------------------------------------- inputs
+
+def decode_inputs(dev, B, hq, hkv, lo, hi, pool_blocks, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(lo, hi + 1, (B,), generator=g, dtype=torch.int32)
+    need = [math.ceil(int(c) / BS) for c in ctx]
+    width = max(need)
+    perm = torch.randperm(pool_blocks, generator=g)
+    bt = torch.full((B, width), -1, dtype=torch.int32)
+    pos = 0
+    for i, n in enumerate(need):
+        bt[i, :n] = perm[pos:pos + n].to(torch.int32)
+        pos += n
+    dg = torch.Generator(device=dev).manual_seed(seed)
+    kc = torch.randn(pool_blocks, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(pool_blocks, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(B, hq, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    return dict(q=q, kc=kc, vc=vc, ctx=ctx.to(dev), bt=bt.to(dev), ctx_host=ctx, bt_host=bt,
+                hq=hq, hkv=hkv)
+
+
+def time_launches(fn, steps: int, warmup: int):
+    """Average ms per call over `steps` calls, HIP events on the current (launch) stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+# ----------------------------------------------------------------------------- workloads
+
+def bench_decode(dev, steps, warmup, shape):
+    from kavor_amd.layers.attention import paged_decode, reserve_decode_workspace
+    from oracle.kvpath_oracle import decode_bytes
+
+    if shape == "qwen3_0.6b":
+        inp = decode_inputs(dev, 256, 16, 8, 100, 2048, 4096)
+    else:
+        inp = decode_inputs(dev, 128, 32, 8, 1024, 32768, 20000)
+    B = inp["q"].shape[0]
+    out = torch.empty_like(inp["q"])
+    reserve_decode_workspace(B, inp["hq"], D, inp["bt"].shape[1], dev)
+
+    def step():
+        paged_decode(inp["q"], inp["kc"], inp["vc"], inp["ctx"], inp["bt"], SCALE, out=out)
+
+    ms = time_launches(step, steps, warmup)
+    nbytes = decode_bytes(inp["ctx_host"].tolist(), inp["hq"], inp["hkv"], D, BS)
+    return inp, dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+
+
+def bench_append(dev, steps, warmup):
+    from kavor_amd.layers.attention import store_kvcache
+    from oracle.kvpath_oracle import append_bytes
+
+    n, hkv, nb = 4096, 8, 512
+    g = torch.Generator().manual_seed(0)
+    dg = torch.Generator(device=dev).manual_seed(0)
+    kc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    # 24 input sets (384 MiB) rotate so that reads come from HBM, not the 256 MiB MALL
+    sets = []
+    for _ in range(24):
+        slots = torch.cat([torch.randperm(nb * BS, generator=g)[:n - 128].to(torch.int32),
+                           torch.full((128,), -1, dtype=torch.int32)])
+        sets.append((torch.randn(n, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16),
+                     torch.randn(n, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16),
+                     slots.to(dev)))
+    it = [0]
+
+    def step():
+        k, v, s = sets[it[0] % len(sets)]
+        it[0] += 1
+        store_kvcache(k, v, kc, vc, s)
+
+    ms = time_launches(step, max(steps, 48), warmup)
+    nbytes = append_bytes(sets[0][2].cpu().numpy(), hkv, D)
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+
+
+def bench_prefill(dev, steps, warmup):
+    from kavor_amd.layers.attention import varlen_prefill
+    from oracle.kvpath_oracle import prefill_flops
+
+    g = torch.Generator().manual_seed(0)
+    hq, hkv, nb = 16, 8, 4096
+    perm = torch.randperm(nb, generator=g).tolist()
+    qlens, klens, tables, pos = [], [], [], 0
+    for _ in range(8):
+        p = 256 * int(torch.randint(0, 17, (1,), generator=g))
+        shared = perm[pos:pos + p // BS]
+        pos += p // BS
+        for _ in range(4):
+            n = int(torch.randint(100, 1025, (1,), generator=g))
+            own = perm[pos:pos + math.ceil((p + n) / BS) - len(shared)]
+            pos += len(own)
+            qlens.append(n)
+            klens.append(p + n)
+            tables.append(shared + own)
+    width = max(len(t) for t in tables)
+    bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.int32, device=dev)
+    cq = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0)), dtype=torch.int32, device=dev)
+    ck = torch.tensor([0] + list(torch.tensor(klens).cumsum(0)), dtype=torch.int32, device=dev)
+    dg = torch.Generator(device=dev).manual_seed(0)
+    kc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(sum(qlens), hq, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+
+    def step():
+        varlen_prefill(q, kc, vc, max(qlens), cq, max(klens), ck, SCALE, causal=True, block_table=bt, out=out)
+
+    ms = time_launches(step, steps, warmup)
+    flops = prefill_flops(cq.cpu().tolist(), ck.cpu().tolist(), hq, D)
+    return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9)
+
+
+def cpu_baseline_decode(inp, budget_s: float = 20.0):
+    """The oracle's bf16 gather + SDPA (a PyTorch-eager port of the reference path) on the
+    host cores, over the first sequences of the headline workload."""
+    from oracle.kvpath_oracle import sdpa_paged_decode, decode_bytes
+
+    nseq = 32  # torch keeps its default thread count (OMP_NUM_THREADS, the host's CPU share)
+    ctx = inp["ctx_host"][:nseq]
+    bt = inp["bt_host"][:nseq]
+    ids = sorted({int(x) for x in bt.flatten() if x >= 0})
+    remap = {b: i for i, b in enumerate(ids)}
+    sel = torch.tensor(ids, dtype=torch.long, device=inp["kc"].device)
+    kc, vc = inp["kc"][sel].cpu(), inp["vc"][sel].cpu()
+    bt_c = bt.clone().apply_(lambda x: remap.get(x, -1))
+    q = inp["q"][:nseq].cpu()
+    sdpa_paged_decode(q, kc, vc, bt_c, ctx, SCALE)  # warm-up
+    times, t_end = [], time.perf_counter() + budget_s
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        sdpa_paged_decode(q, kc, vc, bt_c, ctx, SCALE)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and len(times) >= 5:
+            break
+    sec = statistics.median(times)
+    nbytes = decode_bytes(ctx.tolist(), inp["hq"], inp["hkv"], D, BS)
+    return dict(value=round(nbytes / sec / 1e9, 4), unit="GB/s", cores=torch.get_num_threads(),
+                kind="port",
+                sample=f"first {nseq} of 256 sequences ({int(ctx.sum())} cached tokens), "
+                       f"torch {torch.__version__} bf16 SDPA on {platform.processor() or platform.machine()}, "
+                       f"median of {len(times)} runs")
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled
+    by the plain-copy calibration), committed as profiles/<name>.json; None if absent."""
+    path = ROOT / "profiles" / f"{name}.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get("traffic_bytes")
+    except (ValueError, OSError):
+        return None
+
+
+# ----------------------------------------------------------------------------- main
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extras", action="store_true", help="headline decode workload only")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU's paged KV-cache kernels; --gpus {args.gpus} is not "
+              "supported (the path shards by kv head with no exchange inside attention).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    from kavor_amd._lib import lib
+
+    lib()
+
+    inp, dec = bench_decode(dev, args.steps, args.warmup, "qwen3_0.6b")
+    extras = {}
+    if not args.no_extras:
+        a = bench_append(dev, args.steps, args.warmup)
+        extras["kv_append"] = dict(gbs=round(a["gbs"], 1), frac=round(a["gbs"] / HBM_PEAK_GBS, 4),
+                                   us=round(a["ms"] * 1e3, 3), bytes=a["bytes"],
+                                   workload="4096 tok x 8 kv heads x 128 bf16, 3968 valid + 128 pad slots, "
+                                            "cache [512,256,8,128], 24 rotating input sets")
+        p = bench_prefill(dev, max(5, args.steps // 5), 2)
+        extras["varlen_prefill"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                        ms=round(p["ms"], 4), flops=p["flops"],
+                                        workload="32 seqs, new 100-1024, prefix 0-4096 shared by groups of 4, 16q/8kv")
+        _, c = bench_decode(dev, max(10, args.steps // 2), 3, "qwen3_8b")
+        extras["paged_decode_qwen3_8b"] = dict(gbs=round(c["gbs"], 1), frac=round(c["gbs"] / HBM_PEAK_GBS, 4),
+                                               ms=round(c["ms"], 4), bytes=c["bytes"],
+                                               workload="B=128, 32q/8kv, ctx U[1024,32768], pool 20000 blocks")
+        torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else cpu_baseline_decode(inp)
+
+    gbs = dec["gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "paged decode, Qwen3-0.6B layer: B=256, 16q/8kv heads, head_dim 128, "
+                               "ctx U[100,2048], block 256, pool 4096 blocks",
+                   "bytes_per_step": dec["bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic("paged_decode_qwen3_0.6b_pmc")},
+        "cpu_baseline": cpu,
+        **extras,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,155 @@
+/*
+ * kvpath.h - C ABI of the MI355X (gfx950) paged KV-cache library, libkvpath.so.
+ *
+ * The library implements the three device operations of Kavor's paged KV-cache
+ * path:
+ *
+ *   kvp_append_bf16          replaces the Triton kernel store_kvcache_kernel and its
+ *                            wrapper store_kvcache
+ *                            (kavor/layers/attention/flash_attention_kvcache.py:10-46)
+ *   kvp_paged_decode_bf16    replaces flash_attn_with_kvcache(q.unsqueeze(1), k_cache,
+ *                            v_cache, cache_seqlens, block_table, softmax_scale,
+ *                            causal=True)  (flash_attention_kvcache.py:80-83)
+ *   kvp_varlen_prefill_bf16  replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q,
+ *                            cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+ *                            causal=True, block_table)  (flash_attention_kvcache.py:73-79)
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are passed as a device pointer plus element strides (not bytes).
+ *     bf16 data is passed as void*; the innermost (head_dim) stride is always 1.
+ *   - A paged cache is [num_blocks, block_size, num_kv_heads, head_dim] with strides
+ *     (block_stride, slot_stride, head_stride, 1).  K and V share one stride set; in
+ *     Kavor's page pool K and V are interleaved per page, so block_stride is
+ *     2*block_size*num_kv_heads*head_dim (kavor/engine/cache_pool.py:311-322).
+ *   - Every pointer must be 16-byte aligned and every stride a multiple of 8 elements
+ *     (the kernels move 16-byte vectors).  head_dim must be 64, 128 or 256 for the
+ *     append and 128 for attention.
+ *   - Work is enqueued on `stream` (a hipStream_t; pass the current torch stream).
+ *     Nothing is allocated, freed or synchronised, so every entry point may be
+ *     captured into a hipGraph; all per-step metadata is read from device memory.
+ *   - Return value: 0 on success, a negative KVP_E* code when the arguments are
+ *     rejected on the host (nothing was launched), or a positive hipError_t when a
+ *     launch failed.  kvp_last_error() describes the last failure on this thread.
+ */
+#ifndef KAVOR_AMD_KVPATH_H
+#define KAVOR_AMD_KVPATH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVP_OK 0
+#define KVP_EINVAL (-1)        /* bad shape, stride, alignment or null pointer */
+#define KVP_EUNSUPPORTED (-2)  /* valid but not implemented (head_dim, GQA ratio) */
+#define KVP_EWORKSPACE (-3)    /* decode workspace smaller than required */
+
+/* Message for the last failing call on the calling thread ("" if none). */
+const char* kvp_last_error(void);
+
+/* Library version string, e.g. "kvpath 0.1 gfx950". */
+const char* kvp_version(void);
+
+/*
+ * KV append: for token i with s = slot_mapping[i], copy key[i] (num_kv_heads x
+ * head_dim) to k_cache[s / block_size, s % block_size] and value[i] to
+ * v_cache[...] bit for bit.  s == -1 marks a padding token and is skipped; so is
+ * any other s outside [0, num_cache_slots) (the reference leaves that undefined).
+ * Replaces store_kvcache (flash_attention_kvcache.py:37-46), which takes the key
+ * and value row strides separately (Qwen3: 1024 and 4096 elements,
+ * kavor/models/qwen3.py:80-87) and one block stride for both caches.
+ * Duplicate slots are allowed (graph capture writes slot 0 for every row); which
+ * writer wins is unspecified, as in the reference.
+ */
+int kvp_append_bf16(const void* key, int64_t key_tok_stride, int64_t key_head_stride,
+                    const void* value, int64_t value_tok_stride, int64_t value_head_stride,
+                    void* k_cache, void* v_cache,
+                    int64_t cache_block_stride, int64_t cache_slot_stride,
+                    int64_t cache_head_stride, int64_t num_cache_slots,
+                    const int32_t* slot_mapping, int32_t num_tokens,
+                    int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                    void* stream);
+
+/*
+ * Bytes of device workspace kvp_paged_decode_bf16 needs for up to max_num_seqs
+ * sequences whose block tables are max_blocks_per_seq wide.  The caller allocates
+ * it once (before any graph capture) and passes it on every call; its contents
+ * need no initialisation.  Sequences whose context fits one split never touch it.
+ */
+size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q_heads,
+                                  int32_t head_dim, int32_t max_blocks_per_seq);
+
+/*
+ * Paged decode attention, one query token per sequence:
+ *   out[b, h] = softmax(scale * q[b, h] . K_b^T) V_b
+ * where K_b / V_b are the first context_lens[b] logical tokens of sequence b,
+ * token t living at slot t % block_size of block block_tables[b, t / block_size],
+ * and query head h reads kv head h / (num_q_heads / num_kv_heads) (GQA).
+ * Replaces flash_attn_with_kvcache(..., causal=True) with one query token
+ * (flash_attention_kvcache.py:80-83; the causal flag is a no-op for q_len 1).
+ * Block-table entries at index >= ceil(context_lens[b] / block_size) are never
+ * read (they are stale inside captured graphs, model_runner.py:235).
+ * context_lens[b] == 0 writes zeros (graph padding rows).  A needed block id
+ * outside [0, num_cache_blocks) or a context longer than
+ * max_blocks_per_seq * block_size makes that sequence's output NaN instead of
+ * reading out of bounds.  block_size must be a multiple of 64.
+ * The output row of head h is out + b*out_seq_stride + h*out_head_stride.
+ */
+int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                          const void* k_cache, const void* v_cache,
+                          int64_t cache_block_stride, int64_t cache_slot_stride,
+                          int64_t cache_head_stride, int32_t num_cache_blocks,
+                          const int32_t* block_tables, int64_t block_table_stride,
+                          const int32_t* context_lens, int32_t num_seqs,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t max_blocks_per_seq,
+                          float softmax_scale,
+                          void* out, int64_t out_seq_stride, int64_t out_head_stride,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Variable-length prefill attention over packed sequences (bf16 MFMA).
+ * Sequence s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1]) of q and keys
+ * 0 .. klen_s-1 with klen_s = cu_seqlens_k[s+1] - cu_seqlens_k[s].  With causal != 0
+ * the mask is bottom-right aligned: query i (0-based within the sequence, qlen_s
+ * queries) sees key j iff j <= i + klen_s - qlen_s (flash-attn >= 2.1 semantics;
+ * the reference pins flash-attn 2.8.3.post2, setup.py:10).  Rows that see no key
+ * are written as zeros.
+ *
+ * K/V source:
+ *   block_tables == NULL  dense mode: key j of sequence s is row cu_seqlens_k[s] + j
+ *                         of k / v ([total_k, num_kv_heads, head_dim]); the block
+ *                         strides are ignored.
+ *   block_tables != NULL  paged mode: k / v are the caches and key j of sequence s
+ *                         lives at slot j % block_size of block
+ *                         block_tables[s, j / block_size] (prefix-cached prefill,
+ *                         flash_attention_kvcache.py:74-75).  A needed block id
+ *                         outside [0, num_cache_blocks) or klen_s larger than
+ *                         max_blocks_per_seq * block_size makes that sequence's
+ *                         output NaN.  block_size must be a multiple of 64.
+ * max_seqlen_q bounds every qlen_s (it sizes the grid); sequences longer than it
+ * produce NaN.  Replaces flash_attn_varlen_func(..., causal=True, block_table)
+ * (flash_attention_kvcache.py:76-79).
+ */
+int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                            const void* k, int64_t k_block_stride, int64_t k_tok_stride,
+                            int64_t k_head_stride,
+                            const void* v, int64_t v_block_stride, int64_t v_tok_stride,
+                            int64_t v_head_stride,
+                            const int32_t* block_tables, int64_t block_table_stride,
+                            int32_t num_cache_blocks, int32_t block_size,
+                            int32_t max_blocks_per_seq,
+                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                            int32_t num_seqs, int32_t max_seqlen_q,
+                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                            float softmax_scale, int32_t causal,
+                            void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KAVOR_AMD_KVPATH_H */

@@ -1,0 +1,378 @@
+// Variable-length causal prefill attention (bf16 MFMA), dense or paged K/V.
+//
+// Restates flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+// max_seqlen_k, softmax_scale, causal=True, block_table) as called at
+// kavor/layers/attention/flash_attention_kvcache.py:76-79: dense K/V for prefills with
+// no cached prefix, the paged caches (block_table) when any sequence has a prefix-cache
+// hit (flash_attention_kvcache.py:74-75, model_runner.py:432-433).  The causal mask is
+// bottom-right aligned (flash-attn >= 2.1; the reference pins 2.8.3.post2, setup.py:10).
+//
+// Tiling (gfx950, wave64, v_mfma_f32_32x32x16_bf16)
+//   A workgroup (4 waves) owns one (sequence, kv head, query tile) and all G query heads
+//   of that kv head: 128 "rows" = 128/G query tokens x G heads, row rho = tok*G + g, so a
+//   staged K/V tile feeds G heads.  Wave w owns rows [32w, 32w+32).
+//   Per 64-key tile the workgroup stages K row-major and V transposed in LDS, then each
+//   wave computes S^T = K Q^T (M = 64 keys, N = 32 rows, K-dim = 128) and
+//   O^T += V^T P^T (M = 128 dims, N = 32 rows, K-dim = 64 keys).  With the transposed
+//   products every lane holds whole columns of its own query row (row = lane % 32), so
+//   the online-softmax max / sum / rescale need only one cross-lane exchange (lane^32)
+//   and P feeds the second MFMA straight from registers.
+//   Q stays in registers for the whole key loop (8 x 16 bytes per lane).
+//   The 1-D grid is remapped so that consecutive work items (the query tiles of one
+//   sequence and kv head, and neighbouring sequences that share prefix blocks) run on
+//   the same XCD and share its L2; within a (sequence, kv head) the longest (last)
+//   query tiles are dispatched first.
+#include <math.h>
+
+#include "common.h"
+
+namespace kvp {
+
+constexpr int kPrefillHeadDim = 128;
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows (token x head) per workgroup
+constexpr int kKeyTile = 64;
+constexpr int kKStride = kPrefillHeadDim + 8;  // LDS row pitch of the K tile (bf16)
+constexpr int kVtStride = kKeyTile + 8;        // LDS row pitch of the transposed V tile (bf16)
+constexpr int kNumXcd = 8;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+struct PrefillParams {
+  const uint16_t* q;
+  int64_t q_tok_stride, q_head_stride;
+  const uint16_t* k;
+  int64_t k_blk_stride, k_tok_stride, k_head_stride;
+  const uint16_t* v;
+  int64_t v_blk_stride, v_tok_stride, v_head_stride;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int32_t num_cache_blocks;
+  int32_t block_size;
+  int32_t max_blocks;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int32_t num_tiles;  // query tiles per (sequence, kv head) covered by the grid
+  int32_t num_kv_heads;
+  int32_t total_work;
+  float scale_log2;
+  uint16_t* out;
+  int64_t o_tok_stride, o_head_stride;
+};
+
+__device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <int G, bool PAGED, bool CAUSAL>
+__global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(const PrefillParams p) {
+  constexpr int D = kPrefillHeadDim;
+  constexpr int TOK = kPrefillRows / G;  // query tokens per tile
+
+  // XCD-aware work index: hardware places workgroup id i on XCD i % 8.
+  const int per_xcd = (p.total_work + kNumXcd - 1) / kNumXcd;
+  const int work = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+  if (work >= p.total_work) return;
+  const int tile_slot = work % p.num_tiles;
+  const int kvh = (work / p.num_tiles) % p.num_kv_heads;
+  const int s = work / (p.num_tiles * p.num_kv_heads);
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int n = lane & 31;   // this lane's query row within the wave
+  const int hf = lane >> 5;  // which half of the MFMA K-dim this lane feeds
+
+  const int q_start = p.cu_q[s];
+  const int qlen = p.cu_q[s + 1] - q_start;
+  const int k_start = p.cu_k[s];
+  const int klen = p.cu_k[s + 1] - k_start;
+  const int diag = klen - qlen;  // bottom-right causal offset
+
+  bool bad = false;
+  if (PAGED && klen > p.max_blocks * p.block_size) bad = true;
+
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[kKeyTile * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * kVtStride];
+  __shared__ int s_bad;
+
+  if (tid == 0) s_bad = 0;  // sticky for the workgroup: one sequence, one block table
+  __syncthreads();
+
+  const int ntiles_seq = (qlen + TOK - 1) / TOK;
+  // Grid-stride over query tiles (a sequence longer than the grid's max_seqlen_q is
+  // still covered); the last (longest) tiles go first.
+  for (int t = tile_slot; t < ntiles_seq; t += p.num_tiles) {
+    const int tile = ntiles_seq - 1 - t;
+    const int q0 = tile * TOK;
+
+    // This lane's query row.
+    const int rho = 32 * wave + n;
+    const int tq = rho / G;
+    const int g = rho - tq * G;
+    const int qi = q0 + tq;  // query index within the sequence
+    const bool row_valid = qi < qlen;
+
+    uint4 qreg[D / 16];
+    {
+      const uint16_t* qp = p.q + static_cast<int64_t>(q_start + qi) * p.q_tok_stride +
+                           static_cast<int64_t>(kvh * G + g) * p.q_head_stride + 8 * hf;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+        qreg[ks] = row_valid ? *reinterpret_cast<const uint4*>(qp + 16 * ks) : make_uint4(0, 0, 0, 0);
+    }
+
+    const int q_last = min(qlen, q0 + TOK) - 1;
+    const int kv_end = CAUSAL ? min(klen, q_last + diag + 1) : klen;
+
+    f32x16_t oacc[D / 32];
+#pragma unroll
+    for (int mb = 0; mb < D / 32; ++mb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) oacc[mb][j] = 0.f;
+    float m_run = kMaxFloor, l_run = 0.f;
+    const int row_limit = CAUSAL ? qi + diag : klen - 1;  // last key this row may see
+
+    for (int kv0 = 0; kv0 < kv_end; kv0 += kKeyTile) {
+      __syncthreads();  // previous tile fully consumed
+      // ---- stage K (row-major) and V (transposed) for keys [kv0, kv0 + 64)
+      {
+        const int chunk = tid & 15;
+        int64_t kbase = 0, vbase = 0;
+        bool blk_ok = true;
+        if (PAGED) {
+          const int lblk = kv0 / p.block_size;
+          int blk = (lblk < p.max_blocks) ? p.block_tables[s * p.bt_stride + lblk] : -1;
+          if (blk < 0 || blk >= p.num_cache_blocks) {
+            blk_ok = false;
+            blk = 0;
+          }
+          const int off = kv0 - lblk * p.block_size;
+          kbase = static_cast<int64_t>(blk) * p.k_blk_stride + static_cast<int64_t>(off) * p.k_tok_stride;
+          vbase = static_cast<int64_t>(blk) * p.v_blk_stride + static_cast<int64_t>(off) * p.v_tok_stride;
+        } else {
+          kbase = static_cast<int64_t>(k_start + kv0) * p.k_tok_stride;
+          vbase = static_cast<int64_t>(k_start + kv0) * p.v_tok_stride;
+        }
+        if (!blk_ok) bad = true;
+        kbase += static_cast<int64_t>(kvh) * p.k_head_stride + 8 * chunk;
+        vbase += static_cast<int64_t>(kvh) * p.v_head_stride + 8 * chunk;
+        uint4 kc[4], vc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int key = (tid >> 4) + 16 * u;
+          const bool ok = kv0 + key < klen && blk_ok;
+          kc[u] = ok ? *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride) : make_uint4(0, 0, 0, 0);
+          vc[u] = ok ? *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int key = (tid >> 4) + 16 * u;
+          *reinterpret_cast<uint4*>(&s_k[key * kKStride + 8 * chunk]) = kc[u];
+          const u32 w[4] = {vc[u].x, vc[u].y, vc[u].z, vc[u].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s_vt[(8 * chunk + 2 * e) * kVtStride + key] = static_cast<uint16_t>(w[e] & 0xffffu);
+            s_vt[(8 * chunk + 2 * e + 1) * kVtStride + key] = static_cast<uint16_t>(w[e] >> 16);
+          }
+        }
+      }
+      __syncthreads();
+
+      // ---- S^T = K Q^T : two 32-key blocks, lane holds keys of its own query row
+      f32x16_t sacc[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sacc[mb][j] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+          const uint4 a = *reinterpret_cast<const uint4*>(&s_k[(32 * mb + n) * kKStride + 16 * ks + 8 * hf]);
+          sacc[mb] = mfma32(a, qreg[ks], sacc[mb]);
+        }
+      }
+
+      // ---- online softmax over this tile (base 2)
+      float mx = kMaxFloor;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = kv0 + 32 * mb + 8 * (j >> 2) + 4 * hf + (j & 3);
+          const bool ok = key < klen && key <= row_limit;
+          const float x = ok ? sacc[mb][j] * p.scale_log2 : -INFINITY;
+          sacc[mb][j] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      float rsum = 0.f;
+      u32 pk[2][8];  // P as packed bf16 pairs: [mb][pair]
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+          const float p0 = fast_exp2(sacc[mb][j] - m_new);
+          const float p1 = fast_exp2(sacc[mb][j + 1] - m_new);
+          rsum += p0 + p1;
+          pk[mb][j >> 1] = pack_bf16x2(p0, p1);
+        }
+      rsum += __shfl_xor(rsum, 32);
+      l_run = l_run * alpha + rsum;
+#pragma unroll
+      for (int mb = 0; mb < D / 32; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) oacc[mb][j] *= alpha;
+
+      // ---- O^T += V^T P^T : K-dim step kk covers keys 16kk..16kk+15.  This lane's P
+      // registers for that step hold key offsets {4hf+0..3, 8+4hf+0..3}; the V^T operand
+      // is read with the same key order.
+#pragma unroll
+      for (int kk = 0; kk < kKeyTile / 16; ++kk) {
+        const int mbs = kk >> 1;
+        const int pj = (kk & 1) * 4;  // first packed pair of this step within pk[mbs]
+        const uint4 b = make_uint4(pk[mbs][pj], pk[mbs][pj + 1], pk[mbs][pj + 2], pk[mbs][pj + 3]);
+#pragma unroll
+        for (int mb = 0; mb < D / 32; ++mb) {
+          const uint16_t* vrow = &s_vt[(32 * mb + n) * kVtStride + 16 * kk + 4 * hf];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+          oacc[mb] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), b, oacc[mb]);
+        }
+      }
+    }
+    __syncthreads();
+    if (bad) s_bad = 1;
+    __syncthreads();
+
+    // ---- write O: lane holds dims 32mb + 8(j/4) + 4hf + (j%4) of its query row
+    if (row_valid) {
+      const bool poisoned = s_bad != 0;
+      const float inv = poisoned ? NAN : (l_run > 0.f ? 1.f / l_run : 0.f);
+      uint16_t* op = p.out + static_cast<int64_t>(q_start + qi) * p.o_tok_stride +
+                     static_cast<int64_t>(kvh * G + g) * p.o_head_stride;
+#pragma unroll
+      for (int mb = 0; mb < D / 32; ++mb)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          const int d0 = 32 * mb + 8 * jq + 4 * hf;
+          const uint2 w = make_uint2(pack_bf16x2(oacc[mb][4 * jq] * inv, oacc[mb][4 * jq + 1] * inv),
+                                     pack_bf16x2(oacc[mb][4 * jq + 2] * inv, oacc[mb][4 * jq + 3] * inv));
+          *reinterpret_cast<uint2*>(op + d0) = w;
+        }
+    }
+  }
+}
+
+template <int G>
+static void launch_prefill(bool paged, bool causal, dim3 grid, hipStream_t s, const PrefillParams& p) {
+  const dim3 block(64 * kPrefillWaves);
+  if (paged) {
+    if (causal) hipLaunchKernelGGL((varlen_prefill_kernel<G, true, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((varlen_prefill_kernel<G, true, false>), grid, block, 0, s, p);
+  } else {
+    if (causal) hipLaunchKernelGGL((varlen_prefill_kernel<G, false, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((varlen_prefill_kernel<G, false, false>), grid, block, 0, s, p);
+  }
+}
+
+}  // namespace kvp
+
+using namespace kvp;
+
+extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                       const void* k, int64_t k_block_stride, int64_t k_tok_stride,
+                                       int64_t k_head_stride,
+                                       const void* v, int64_t v_block_stride, int64_t v_tok_stride,
+                                       int64_t v_head_stride,
+                                       const int32_t* block_tables, int64_t block_table_stride,
+                                       int32_t num_cache_blocks, int32_t block_size,
+                                       int32_t max_blocks_per_seq,
+                                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                       int32_t num_seqs, int32_t max_seqlen_q,
+                                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                       float softmax_scale, int32_t causal,
+                                       void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                                       void* stream) {
+  clear_error();
+  if (num_seqs < 0 || max_seqlen_q < 0)
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: num_seqs=%d max_seqlen_q=%d", num_seqs, max_seqlen_q);
+  if (num_seqs == 0 || max_seqlen_q == 0) return KVP_OK;
+  if (head_dim != kPrefillHeadDim)
+    return fail(KVP_EUNSUPPORTED, "kvp_varlen_prefill_bf16: head_dim=%d (supported: 128)", head_dim);
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: num_q_heads=%d not a multiple of num_kv_heads=%d",
+                num_q_heads, num_kv_heads);
+  const int G = num_q_heads / num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(KVP_EUNSUPPORTED, "kvp_varlen_prefill_bf16: GQA ratio %d (supported: 1, 2, 4, 8)", G);
+  const bool paged = block_tables != nullptr;
+  if (paged) {
+    if (block_size <= 0 || block_size % kKeyTile != 0)
+      return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: block_size=%d must be a positive multiple of 64",
+                  block_size);
+    if (max_blocks_per_seq <= 0 || num_cache_blocks <= 0 || block_table_stride < max_blocks_per_seq)
+      return fail(KVP_EINVAL,
+                  "kvp_varlen_prefill_bf16: max_blocks_per_seq=%d num_cache_blocks=%d block_table_stride=%lld",
+                  max_blocks_per_seq, num_cache_blocks, static_cast<long long>(block_table_stride));
+    if (reinterpret_cast<uintptr_t>(block_tables) & 3u)
+      return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: block_tables must be 4-byte aligned");
+    if (!mult8(k_block_stride) || !mult8(v_block_stride))
+      return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: block strides must be multiples of 8 elements");
+  }
+  if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out)
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: null pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: q/k/v must be 16-byte and out 8-byte aligned");
+  if (!mult8(q_tok_stride) || !mult8(q_head_stride) || !mult8(k_tok_stride) || !mult8(k_head_stride) ||
+      !mult8(v_tok_stride) || !mult8(v_head_stride) || (out_tok_stride & 3) || (out_head_stride & 3))
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: q/k/v strides must be multiples of 8, out of 4 elements");
+
+  const int tok_per_tile = kPrefillRows / G;
+  const int64_t num_tiles = (static_cast<int64_t>(max_seqlen_q) + tok_per_tile - 1) / tok_per_tile;
+  const int64_t total = num_tiles * num_kv_heads * num_seqs;
+  if (total > (1ll << 30)) return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: grid too large");
+
+  PrefillParams p;
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_tok_stride = q_tok_stride;
+  p.q_head_stride = q_head_stride;
+  p.k = static_cast<const uint16_t*>(k);
+  p.k_blk_stride = k_block_stride;
+  p.k_tok_stride = k_tok_stride;
+  p.k_head_stride = k_head_stride;
+  p.v = static_cast<const uint16_t*>(v);
+  p.v_blk_stride = v_block_stride;
+  p.v_tok_stride = v_tok_stride;
+  p.v_head_stride = v_head_stride;
+  p.block_tables = block_tables;
+  p.bt_stride = block_table_stride;
+  p.num_cache_blocks = num_cache_blocks;
+  p.block_size = paged ? block_size : kKeyTile;
+  p.max_blocks = max_blocks_per_seq;
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.num_tiles = static_cast<int32_t>(num_tiles);
+  p.num_kv_heads = num_kv_heads;
+  p.total_work = static_cast<int32_t>(total);
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  p.out = static_cast<uint16_t*>(out);
+  p.o_tok_stride = out_tok_stride;
+  p.o_head_stride = out_head_stride;
+
+  const int per_xcd = static_cast<int>((total + kNumXcd - 1) / kNumXcd);
+  const dim3 grid(per_xcd * kNumXcd);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool c = causal != 0;
+  switch (G) {
+    case 1: launch_prefill<1>(paged, c, grid, s, p); break;
+    case 2: launch_prefill<2>(paged, c, grid, s, p); break;
+    case 4: launch_prefill<4>(paged, c, grid, s, p); break;
+    default: launch_prefill<8>(paged, c, grid, s, p); break;
+  }
+  return launch_status("kvp_varlen_prefill_bf16");
+}

@@ -1,0 +1,104 @@
+"""CPU checks of the C ABI: libkvpath.so loads, exports exactly what include/kvpath.h
+declares, and rejects bad arguments on the host before launching anything (these calls
+make no HIP API call, so they run without a GPU)."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from kavor_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "kvpath.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(kvp_\w+)\s*\(", text)))
+
+
+def test_header_matches_binding_table():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True)
+    exported = set(re.findall(r"\bT (kvp_\w+)$", nm.stdout, flags=re.M))
+    assert exported == set(declared_functions())
+
+
+def test_version_string():
+    assert _lib.version().startswith("kvpath ")
+
+
+def _append(**over):
+    args = dict(key=16, kts=1024, khs=128, value=16, vts=4096, vhs=128, kc=16, vc=16,
+                bstr=524288, sstr=1024, hstr=128, nslots=1 << 17, slots=16, n=4,
+                hkv=8, d=128, bs=256, stream=None)
+    args.update(over)
+    return _lib.lib().kvp_append_bf16(*args.values())
+
+
+def test_append_rejects_bad_arguments_on_host():
+    lib = _lib.lib()
+    assert _append(n=0) == _lib.KVP_OK                       # nothing to do
+    assert _append(d=96) == _lib.KVP_EUNSUPPORTED
+    assert b"head_dim=96" in lib.kvp_last_error()
+    assert _append(key=8) == _lib.KVP_EINVAL                 # misaligned pointer
+    assert _append(vts=4100) == _lib.KVP_EINVAL              # stride not a multiple of 8
+    assert _append(slots=0) == _lib.KVP_EINVAL               # null slot mapping
+    assert _append(n=-1) == _lib.KVP_EINVAL
+
+
+def _decode(**over):
+    args = dict(q=16, qs=2048, qh=128, kc=16, vc=16, bstr=524288, sstr=1024, hstr=128, nblk=64,
+                bt=16, bts=16, ctx=16, b=4, hq=16, hkv=8, d=128, bs=256, maxb=16, scale=0.088,
+                out=16, os=2048, oh=128, ws=16, wsb=1 << 30, stream=None)
+    args.update(over)
+    return _lib.lib().kvp_paged_decode_bf16(*args.values())
+
+
+def test_decode_rejects_bad_arguments_on_host():
+    assert _decode(b=0) == _lib.KVP_OK
+    assert _decode(d=64) == _lib.KVP_EUNSUPPORTED
+    assert _decode(hq=12) == _lib.KVP_EINVAL                 # 12 q heads over 8 kv heads
+    assert _decode(hq=24) == _lib.KVP_EUNSUPPORTED           # GQA ratio 3
+    assert _decode(bs=100) == _lib.KVP_EINVAL                # not a multiple of 64
+    assert _decode(bts=8) == _lib.KVP_EINVAL                 # table stride < width
+    assert _decode(wsb=100) == _lib.KVP_EWORKSPACE           # 16 splits need partials
+    assert b"workspace" in _lib.lib().kvp_last_error()
+
+
+def test_decode_workspace_size_formula():
+    # seqs * q heads * max blocks * (head_dim + 2) fp32 values
+    assert _lib.lib().kvp_decode_workspace_bytes(512, 16, 128, 16) == 512 * 16 * 16 * 130 * 4
+    assert _lib.lib().kvp_decode_workspace_bytes(0, 16, 128, 16) == 0
+
+
+def _prefill(**over):
+    args = dict(q=16, qts=2048, qhs=128, k=16, kbs=0, kts=1024, khs=128, v=16, vbs=0, vts=4096,
+                vhs=128, bt=None, bts=0, nblk=0, bs=0, maxb=0, cuq=16, cuk=16, nseq=2, maxq=100,
+                hq=16, hkv=8, d=128, scale=0.088, causal=1, out=16, ots=2048, ohs=128, stream=None)
+    args.update(over)
+    return _lib.lib().kvp_varlen_prefill_bf16(*args.values())
+
+
+def test_prefill_rejects_bad_arguments_on_host():
+    assert _prefill(nseq=0) == _lib.KVP_OK
+    assert _prefill(d=256) == _lib.KVP_EUNSUPPORTED
+    assert _prefill(bt=16, bs=32, maxb=4, bts=4, nblk=8) == _lib.KVP_EINVAL  # paged, bs % 64
+    assert _prefill(kts=1020) == _lib.KVP_EINVAL
+    assert _prefill(cuq=None) == _lib.KVP_EINVAL
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libkvpath.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.lib()

@@ -1,0 +1,206 @@
+"""GPU parity of paged decode (kvp_paged_decode_bf16 via kavor_amd.layers.attention.paged_decode)
+against the fp32 oracle, within atol 2e-2 / rtol 1e-2 on the bf16 output."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kvpath_oracle as ref
+from tests.helpers import TOL, gen, randn_bf16, interleaved_pool, contiguous_caches, random_block_tables, bits_equal
+from tests.test_golden import load, bf16
+
+pytestmark = pytest.mark.gpu
+SCALE = 128 ** -0.5
+
+
+def _decode(q, kc, vc, ctx, bt, scale=SCALE, **kw):
+    from kavor_amd.layers.attention import paged_decode
+
+    return paged_decode(q, kc, vc, cache_seqlens=ctx, block_table=bt, softmax_scale=scale, **kw)
+
+
+def _case(seed, B, hq, hkv, bs, lo, hi, nb=None, layout="contiguous", width=None):
+    g = gen(seed)
+    ctx = torch.randint(lo, hi + 1, (B,), generator=g, dtype=torch.int32)
+    need = sum(math.ceil(int(c) / bs) for c in ctx)
+    nb = nb or need + 3
+    if layout == "contiguous":
+        kc, vc = contiguous_caches(nb, bs, hkv, 128, g)
+    else:
+        _, kc, vc = interleaved_pool(nb, bs, hkv, 128, g)
+    bt = random_block_tables([int(c) for c in ctx], bs, nb, g, width=width)
+    q = randn_bf16((B, hq, 128), g)
+    return q, kc, vc, bt, ctx
+
+
+def _check(dev, q, kc, vc, bt, ctx, tol=TOL):
+    out = _decode(q.to(dev), kc.to(dev), vc.to(dev), ctx.to(dev), bt.to(dev))
+    torch.cuda.synchronize()
+    want = ref.paged_decode(q, kc, vc, bt, ctx, SCALE)
+    torch.testing.assert_close(out.cpu().float(), want, **tol)
+    return out
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+@pytest.mark.parametrize("bs,layout", [(256, "interleaved"), (64, "contiguous"), (128, "interleaved")])
+def test_decode_matches_oracle(cuda_device, G, bs, layout):
+    hkv = 2
+    q, kc, vc, bt, ctx = _case(10 * G + bs, B=12, hq=G * hkv, hkv=hkv, bs=bs, lo=1, hi=1500, layout=layout)
+    _check(cuda_device, q, kc, vc, bt, ctx)
+
+
+def test_decode_4d_query_and_out_buffer(cuda_device):
+    """q given as [B, 1, Hq, D] (the reference's q.unsqueeze(1)) returns [B, 1, Hq, D]; a
+    preallocated, strided out buffer is honoured."""
+    q, kc, vc, bt, ctx = _case(11, B=5, hq=16, hkv=8, bs=256, lo=1, hi=700)
+    d = cuda_device
+    out4 = _decode(q.to(d).unsqueeze(1), kc.to(d), vc.to(d), ctx.to(d), bt.to(d))
+    assert out4.shape == (5, 1, 16, 128)
+    big = torch.full((5, 20, 128), 7.0, dtype=torch.bfloat16, device=d)
+    _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt.to(d), out=big[:, 2:18])
+    torch.cuda.synchronize()
+    assert bits_equal(big[:, 2:18].cpu(), out4[:, 0].cpu())
+    assert torch.all(big[:, :2] == 7.0) and torch.all(big[:, 18:] == 7.0)
+
+
+def test_decode_context_edges(cuda_device):
+    """ctx 0 -> zeros, ctx 1 -> that token's V row exactly, block-boundary lengths."""
+    q, kc, vc, bt, _ = _case(12, B=8, hq=16, hkv=8, bs=256, lo=513, hi=513)
+    ctx = torch.tensor([0, 1, 255, 256, 257, 511, 512, 513], dtype=torch.int32)
+    out = _check(cuda_device, q, kc, vc, bt, ctx).cpu()
+    assert torch.count_nonzero(out[0]) == 0
+    for h in range(16):
+        assert bits_equal(out[1, h], vc[int(bt[1, 0]), 0, h // 2])
+
+
+def test_decode_stale_table_columns_are_not_read(cuda_device):
+    """Graph replay leaves stale block ids past ceil(ctx/bs) (model_runner.py:235); eager
+    pads with -1.  Both, and out-of-range garbage, give identical results."""
+    q, kc, vc, bt, ctx = _case(13, B=16, hq=16, hkv=8, bs=64, lo=1, hi=900, width=20)
+    d = cuda_device
+    base = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt.to(d)).cpu()
+    junk = bt.clone()
+    junk[junk < 0] = torch.randint(-(1 << 30), 1 << 30, (int((junk < 0).sum()),), generator=gen(130), dtype=torch.int32)
+    got = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), junk.to(d)).cpu()
+    assert bits_equal(base, got)
+
+
+def test_decode_invalid_block_poisons_only_its_sequence(cuda_device):
+    q, kc, vc, bt, ctx = _case(14, B=6, hq=16, hkv=8, bs=256, lo=300, hi=900)
+    nb = kc.shape[0]
+    bad = bt.clone()
+    bad[2, 1] = nb + 5      # needed block beyond the pool
+    bad[4, 0] = -3          # negative id
+    d = cuda_device
+    out = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bad.to(d)).cpu().float()
+    assert torch.isnan(out[2]).all() and torch.isnan(out[4]).all()
+    good = [0, 1, 3, 5]
+    want = ref.paged_decode(q[good], kc, vc, bt[good], ctx[good], SCALE)
+    torch.testing.assert_close(out[good], want, **TOL)
+    over = ctx.clone()
+    over[0] = bt.shape[1] * 256 + 1   # longer than the table can describe
+    out2 = _decode(q.to(d), kc.to(d), vc.to(d), over.to(d), bt.to(d)).cpu().float()
+    assert torch.isnan(out2[0]).all() and not torch.isnan(out2[1:]).any()
+
+
+def test_decode_batch_permutation_is_bitwise_invariant(cuda_device):
+    q, kc, vc, bt, ctx = _case(15, B=32, hq=16, hkv=8, bs=256, lo=1, hi=2048)
+    d = cuda_device
+    perm = torch.randperm(32, generator=gen(150))
+    a = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt.to(d)).cpu()
+    b = _decode(q[perm].to(d), kc.to(d), vc.to(d), ctx[perm].to(d), bt[perm].contiguous().to(d)).cpu()
+    assert bits_equal(a[perm], b)
+
+
+def test_decode_split_granularity_stays_within_tolerance(cuda_device):
+    """A wide block table (>32 columns) groups blocks per split; the same sequences then
+    merge fewer partials.  Both layouts agree with the oracle and with each other."""
+    q, kc, vc, bt, ctx = _case(16, B=8, hq=32, hkv=8, bs=256, lo=2000, hi=8192, width=40)
+    d = cuda_device
+    wide = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt.to(d)).cpu().float()
+    narrow = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt[:, :32].contiguous().to(d)).cpu().float()
+    want = ref.paged_decode(q, kc, vc, bt, ctx, SCALE)
+    torch.testing.assert_close(wide, want, **TOL)
+    torch.testing.assert_close(narrow, want, **TOL)
+
+
+def test_decode_graph_replay_matches_eager(cuda_device):
+    """Capture with zero metadata (as capture_cudagraph does), then replay with new
+    lengths and tables: every replay equals the eager call bit for bit."""
+    B, hq, hkv, bs, width = 16, 16, 8, 256, 16
+    g = gen(17)
+    nb = 300
+    d = cuda_device
+    kc, vc = (t.to(d) for t in contiguous_caches(nb, bs, hkv, 128, g))
+    q = randn_bf16((B, hq, 128), g).to(d)
+    ctx_buf = torch.zeros(B, dtype=torch.int32, device=d)
+    bt_buf = torch.zeros(B, width, dtype=torch.int32, device=d)
+    out = _decode(q, kc, vc, ctx_buf, bt_buf)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _decode(q, kc, vc, ctx_buf, bt_buf, out=out)
+    for step in range(3):
+        gs = gen(170 + step)
+        ctx = torch.randint(0, 4096, (B,), generator=gs, dtype=torch.int32)
+        bt = random_block_tables([int(c) for c in ctx], bs, nb, gs, width=width, pad=7)
+        ctx_buf.copy_(ctx.to(d))
+        bt_buf.copy_(bt.to(d))
+        graph.replay()
+        torch.cuda.synchronize()
+        replay = out.clone()
+        eager = _decode(q, kc, vc, ctx_buf, bt_buf)
+        torch.cuda.synchronize()
+        assert bits_equal(replay, eager)
+    torch.testing.assert_close(replay.cpu().float(), ref.paged_decode(q.cpu(), kc.cpu(), vc.cpu(), bt, ctx, SCALE), **TOL)
+
+
+def _sampled_check(dev, q, kc, vc, bt, ctx, out, idx, bs):
+    """Oracle check of a few sequences of a full-size run, gathering only their blocks."""
+    ids, rows = [], []
+    for b in idx:
+        n = math.ceil(int(ctx[b]) / bs)
+        rows.append(list(range(len(ids), len(ids) + n)))
+        ids.extend(int(x) for x in bt[b, :n])
+    sel = torch.tensor(ids, dtype=torch.long, device=dev)
+    kc_s, vc_s = kc[sel].cpu(), vc[sel].cpu()
+    width = max(len(r) for r in rows)
+    bt_s = torch.tensor([r + [-1] * (width - len(r)) for r in rows], dtype=torch.int32)
+    want = ref.paged_decode(q[idx].cpu(), kc_s, vc_s, bt_s, ctx[idx].cpu(), SCALE)
+    torch.testing.assert_close(out[idx].cpu().float(), want, **TOL)
+
+
+@pytest.mark.parametrize("shape", ["qwen3_0.6b", "qwen3_8b"])
+def test_decode_full_size_sampled(cuda_device, shape):
+    """The two decode workloads at full size: Qwen3-0.6B (B=256, 16q/8kv, ctx 100-2048,
+    4096-block pool) and Qwen3-8B (B=128, 32q/8kv, ctx 1024-32768, 20000-block pool).
+    Every output is finite; 12 (0.6B) or 6 (8B) sampled sequences match the oracle."""
+    B, hq, lo, hi, nb = (256, 16, 100, 2048, 4096) if shape == "qwen3_0.6b" else (128, 32, 1024, 32768, 20000)
+    hkv, bs, d = 8, 256, cuda_device
+    g = gen(18)
+    ctx = torch.randint(lo, hi + 1, (B,), generator=g, dtype=torch.int32)
+    bt = random_block_tables([int(c) for c in ctx], bs, nb, g)
+    dg = torch.Generator(device=d).manual_seed(18)
+    kc = torch.randn(nb, bs, hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
+    vc = torch.randn(nb, bs, hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
+    q = randn_bf16((B, hq, 128), g).to(d)
+    out = _decode(q, kc, vc, ctx.to(d), bt.to(d))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    idx = torch.randperm(B, generator=g)[:12 if B == 256 else 6].tolist()
+    _sampled_check(d, q, kc, vc, bt, ctx, out, idx, bs)
+    del kc, vc
+    torch.cuda.empty_cache()
+
+
+def test_decode_golden(cuda_device):
+    f = load("decode_small")
+    d = cuda_device
+    out = _decode(bf16(f["q"]).to(d), bf16(f["k_cache"]).to(d), bf16(f["v_cache"]).to(d),
+                  torch.from_numpy(f["context_lens"]).to(d), torch.from_numpy(f["block_tables"]).to(d),
+                  scale=float(f["scale"]))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().double(), torch.from_numpy(f["out"]), **TOL)
+    # one-token row: exactly the V row
+    assert np.array_equal(out[0].cpu().float().numpy(), f["out"][0].astype(np.float32))

@@ -1,0 +1,196 @@
+"""GPU parity of varlen prefill (kvp_varlen_prefill_bf16 via kavor_amd.layers.attention.varlen_prefill)
+against the fp32 oracle, within atol 2e-2 / rtol 1e-2 on the bf16 output."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kvpath_oracle as ref
+from tests.helpers import TOL, gen, randn_bf16, interleaved_pool, contiguous_caches, random_block_tables, bits_equal
+from tests.test_golden import load, bf16
+
+pytestmark = pytest.mark.gpu
+SCALE = 128 ** -0.5
+
+
+def _prefill(q, k, v, cq, ck, max_q, scale=SCALE, causal=True, bt=None):
+    from kavor_amd.layers.attention import varlen_prefill
+
+    return varlen_prefill(q, k, v, max_seqlen_q=max_q, cu_seqlens_q=cq, max_seqlen_k=0,
+                          cu_seqlens_k=ck, softmax_scale=scale, causal=causal, block_table=bt)
+
+
+def _cu(lens):
+    return torch.tensor(np.cumsum([0] + list(lens)), dtype=torch.int32)
+
+
+def _dense_case(seed, qlens, hq, hkv, qkv_view=True):
+    g = gen(seed)
+    T = sum(qlens)
+    q = randn_bf16((T, hq, 128), g)
+    if qkv_view:  # Qwen3: k fresh, v a view into the fused projection
+        wide = randn_bf16((T, (hq + 2 * hkv) * 128), g)
+        v = wide[:, (hq + hkv) * 128:].view(T, hkv, 128)
+    else:
+        v = randn_bf16((T, hkv, 128), g)
+    k = randn_bf16((T, hkv, 128), g)
+    return q, k, v
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_dense_causal_matches_oracle(cuda_device, G):
+    hkv = 2
+    qlens = [1, 17, 64, 65, 200, 333]
+    q, k, v = _dense_case(100 + G, qlens, G * hkv, hkv)
+    cu = _cu(qlens)
+    d = cuda_device
+    out = _prefill(q.to(d), k.to(d), v.to(d), cu.to(d), cu.to(d), max(qlens))
+    torch.cuda.synchronize()
+    want = ref.varlen_prefill(q, k, v, cu, cu, SCALE)
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
+
+
+def test_dense_noncausal_matches_oracle(cuda_device):
+    qlens = [3, 130, 77]
+    q, k, v = _dense_case(110, qlens, 16, 8, qkv_view=False)
+    cu = _cu(qlens)
+    d = cuda_device
+    out = _prefill(q.to(d), k.to(d), v.to(d), cu.to(d), cu.to(d), max(qlens), causal=False)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), ref.varlen_prefill(q, k, v, cu, cu, SCALE, causal=False), **TOL)
+
+
+def _paged_case(seed, qlens, prefix, hq, hkv, bs, layout="interleaved", nb=None):
+    g = gen(seed)
+    klens = [a + b for a, b in zip(qlens, prefix)]
+    need = sum(math.ceil(k / bs) for k in klens)
+    nb = nb or need + 5
+    if layout == "interleaved":
+        _, kc, vc = interleaved_pool(nb, bs, hkv, 128, g)
+    else:
+        kc, vc = contiguous_caches(nb, bs, hkv, 128, g)
+    bt = random_block_tables(klens, bs, nb, g)
+    q = randn_bf16((sum(qlens), hq, 128), g)
+    return q, kc, vc, bt, _cu(qlens), _cu(klens)
+
+
+@pytest.mark.parametrize("bs,layout", [(256, "interleaved"), (64, "contiguous")])
+@pytest.mark.parametrize("G", [2, 4])
+def test_paged_prefix_matches_oracle(cuda_device, bs, layout, G):
+    """Prefix-cached prefill over the pages: block-aligned prefixes (prefix-cache hits),
+    unaligned ones (chunked prefill, scheduler.py:124) and empty ones in one batch."""
+    qlens = [70, 5, 300, 1, 129]
+    prefix = [256, 37, 0, 511, 1024]
+    q, kc, vc, bt, cq, ck = _paged_case(200 + bs + G, qlens, prefix, G * 2, 2, bs, layout)
+    d = cuda_device
+    out = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
+    torch.cuda.synchronize()
+    want = ref.varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt)
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
+
+
+def test_paged_equals_dense_bitwise(cuda_device):
+    """The same keys read through scattered pages or as packed rows give identical bits."""
+    qlens = [40, 300, 9]
+    q, kc, vc, bt, cq, ck = _paged_case(210, qlens, [0, 0, 0], 16, 8, 256)
+    d = cuda_device
+    kd = torch.cat([ref._gather_tokens(kc, bt[s], qlens[s]) for s in range(3)])
+    vd = torch.cat([ref._gather_tokens(vc, bt[s], qlens[s]) for s in range(3)])
+    paged = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
+    dense = _prefill(q.to(d), kd.to(d), vd.to(d), cq.to(d), ck.to(d), max(qlens))
+    torch.cuda.synchronize()
+    assert bits_equal(paged.cpu(), dense.cpu())
+
+
+def test_grid_smaller_than_longest_sequence(cuda_device):
+    """max_seqlen_q only sizes the grid: an understated value still computes every row."""
+    qlens = [500, 20]
+    q, k, v = _dense_case(220, qlens, 16, 8)
+    cu = _cu(qlens)
+    d = cuda_device
+    out = _prefill(q.to(d), k.to(d), v.to(d), cu.to(d), cu.to(d), 64)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), ref.varlen_prefill(q, k, v, cu, cu, SCALE), **TOL)
+
+
+def test_rows_without_keys_and_empty_sequences(cuda_device):
+    """klen < qlen leaves leading rows with no visible key (zeros); zero-length
+    sequences in the batch are harmless."""
+    g = gen(230)
+    q = randn_bf16((12, 4, 128), g)
+    k, v = randn_bf16((7, 2, 128), g), randn_bf16((7, 2, 128), g)
+    cq, ck = _cu([10, 0, 2]), _cu([5, 0, 2])
+    d = cuda_device
+    out = _prefill(q.to(d), k.to(d), v.to(d), cq.to(d), ck.to(d), 10)
+    torch.cuda.synchronize()
+    want = ref.varlen_prefill(q, k, v, cq, ck, SCALE)
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
+    assert torch.count_nonzero(out[:5].cpu()) == 0
+
+
+def test_invalid_block_poisons_only_its_sequence(cuda_device):
+    qlens, prefix = [50, 60], [256, 256]
+    q, kc, vc, bt, cq, ck = _paged_case(240, qlens, prefix, 16, 8, 256)
+    bad = bt.clone()
+    bad[0, 0] = kc.shape[0] + 3
+    d = cuda_device
+    out = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), 60, bt=bad.to(d)).cpu().float()
+    assert torch.isnan(out[:50]).all()
+    want = ref.varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt)
+    torch.testing.assert_close(out[50:], want[50:], **TOL)
+
+
+def test_full_size_prefix_shared_sampled(cuda_device):
+    """32 sequences, 100-1024 new tokens each, cached prefixes of 0-4096 tokens in whole
+    256-token blocks shared by groups of 4 (identical leading block ids), Qwen3-0.6B heads.
+    All outputs finite; 4 sequences checked against the oracle."""
+    g = gen(250)
+    bs, hkv, hq, d = 256, 8, 16, cuda_device
+    qlens, prefix, tables = [], [], []
+    nb = 4096
+    perm = torch.randperm(nb, generator=g).tolist()
+    pos = 0
+    for grp in range(8):
+        p = 256 * int(torch.randint(0, 17, (1,), generator=g))
+        shared = perm[pos:pos + p // 256]
+        pos += p // 256
+        for _ in range(4):
+            n = int(torch.randint(100, 1025, (1,), generator=g))
+            own = perm[pos:pos + math.ceil((p + n) / bs) - len(shared)]
+            pos += len(own)
+            qlens.append(n)
+            prefix.append(p)
+            tables.append(shared + own)
+    width = max(len(t) for t in tables)
+    bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.int32)
+    cq, ck = _cu(qlens), _cu([a + b for a, b in zip(qlens, prefix)])
+    dg = torch.Generator(device=d).manual_seed(250)
+    kc = torch.randn(nb, bs, hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
+    vc = torch.randn(nb, bs, hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
+    q = randn_bf16((sum(qlens), hq, 128), g).to(d)
+    out = _prefill(q, kc, vc, cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    for s in (0, 5, 17, 31):
+        klen = int(ck[s + 1] - ck[s])
+        nblk = math.ceil(klen / bs)
+        sel = bt[s, :nblk].long().to(d)
+        out_s = ref.varlen_prefill(q[cq[s]:cq[s + 1]].cpu(), kc[sel].cpu(), vc[sel].cpu(),
+                                   _cu([qlens[s]]), _cu([klen]), SCALE,
+                                   block_tables=torch.arange(nblk, dtype=torch.int32).view(1, -1))
+        torch.testing.assert_close(out[cq[s]:cq[s + 1]].cpu().float(), out_s, **TOL)
+    del kc, vc
+    torch.cuda.empty_cache()
+
+
+def test_prefill_golden(cuda_device):
+    f = load("prefill_small")
+    d = cuda_device
+    cq = torch.from_numpy(f["cu_seqlens_q"])
+    out = _prefill(bf16(f["q"]).to(d), bf16(f["k_cache"]).to(d), bf16(f["v_cache"]).to(d),
+                   cq.to(d), torch.from_numpy(f["cu_seqlens_k"]).to(d), int(np.diff(f["cu_seqlens_q"]).max()),
+                   scale=float(f["scale"]), bt=torch.from_numpy(f["block_tables"]).to(d))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().double(), torch.from_numpy(f["out"]), **TOL)
