@@ -87,7 +87,7 @@ def bench_decode(dev, steps, warmup, shape):
         inp = decode_inputs(dev, 128, 32, 8, 1024, 32768, 20000)
     B = inp["q"].shape[0]
     out = torch.empty_like(inp["q"])
-    reserve_decode_workspace(B, inp["hq"], D, inp["bt"].shape[1], dev)
+    reserve_decode_workspace(B, inp["hq"], D, inp["bt"].shape[1], BS, dev)
 
     def step():
         paged_decode(inp["q"], inp["kc"], inp["vc"], inp["ctx"], inp["bt"], SCALE, out=out)

@@ -74,12 +74,14 @@ int kvp_append_bf16(const void* key, int64_t key_tok_stride, int64_t key_head_st
 
 /*
  * Bytes of device workspace kvp_paged_decode_bf16 needs for up to max_num_seqs
- * sequences whose block tables are max_blocks_per_seq wide.  The caller allocates
- * it once (before any graph capture) and passes it on every call; its contents
- * need no initialisation.  Sequences whose context fits one split never touch it.
+ * sequences whose block tables are max_blocks_per_seq wide with block_size-token
+ * blocks.  The caller allocates it once (before any graph capture), 256-byte aligned,
+ * and passes it on every call; its contents need no initialisation.  It holds the
+ * batch's step prefix sums and the fp32 partial states of sequences that the
+ * work split divides.  Returns 0 for arguments the decode does not support.
  */
-size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q_heads,
-                                  int32_t head_dim, int32_t max_blocks_per_seq);
+size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q_heads, int32_t head_dim,
+                                  int32_t max_blocks_per_seq, int32_t block_size);
 
 /*
  * Paged decode attention, one query token per sequence:

@@ -36,7 +36,7 @@ SIGNATURES: dict[str, tuple] = {
         _i32, _i32, _i32,                 # num_kv_heads, head_dim, block_size
         _c_void_p,                        # stream
     ]),
-    "kvp_decode_workspace_bytes": (_size_t, [_i32, _i32, _i32, _i32]),
+    "kvp_decode_workspace_bytes": (_size_t, [_i32, _i32, _i32, _i32, _i32]),
     "kvp_paged_decode_bf16": (ctypes.c_int, [
         _c_void_p, _i64, _i64,            # q, q_seq_stride, q_head_stride
         _c_void_p, _c_void_p,             # k_cache, v_cache

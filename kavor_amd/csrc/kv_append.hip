@@ -8,7 +8,7 @@
 // chunks (8 bf16); the wave's lanes own consecutive chunks, so every load and store
 // is a dwordx4 and a 16-lane group covers one 256-byte head row contiguously.  Each
 // lane issues all of its loads before its first store so a wave keeps up to 4 KiB in
-// flight.  For Qwen3 (8 kv heads x 128) a token is 256 chunks: 4 per lane.
+// flight; the token index, slot and row addresses are wave-uniform scalars.  For Qwen3 (8 kv heads x 128) a token is 256 chunks: 4 per lane.
 #include "common.h"
 
 namespace kvp {
@@ -31,49 +31,68 @@ struct AppendParams {
 constexpr int kAppendWaves = 4;     // tokens per workgroup
 constexpr int kAppendUnroll = 4;    // 16-byte chunks in flight per lane
 
+// Chunk j of a token (K chunks first, then V) -> source and destination offsets in
+// 16-byte units.  `j` is clamped by the caller so every computed address is valid.
+template <int HEAD_DIM>
+__device__ __forceinline__ void chunk_offsets(const AppendParams& p, int j, int chunks_per_tensor,
+                                              bool& is_v, int64_t& src, int64_t& dst) {
+  constexpr int kChunksPerHead = HEAD_DIM / 8;
+  is_v = j >= chunks_per_tensor;
+  const int jj = is_v ? j - chunks_per_tensor : j;
+  const int head = jj / kChunksPerHead;
+  const int part = jj - head * kChunksPerHead;
+  src = head * (is_v ? p.value_head_stride : p.key_head_stride) + part;
+  dst = head * p.head_stride + part;
+}
+
 template <int HEAD_DIM>
 __global__ __launch_bounds__(64 * kAppendWaves) void kv_append_kernel(const AppendParams p) {
-  constexpr int kChunksPerHead = HEAD_DIM / 8;
-  const int tok = blockIdx.x * kAppendWaves + (threadIdx.x >> 6);
+  // Token index and slot are wave-uniform: keep them (and the address math) scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tok = blockIdx.x * kAppendWaves + wave;
   const int lane = threadIdx.x & 63;
   if (tok >= p.num_tokens) return;
   const int32_t slot = p.slot_mapping[tok];
   if (slot < 0 || static_cast<int64_t>(slot) >= p.num_cache_slots) return;  // -1: padding
-  const int32_t blk = slot / p.block_size;
-  const int32_t off = slot - blk * p.block_size;
+  const int bs = p.block_size;
+  int32_t blk, off;
+  if ((bs & (bs - 1)) == 0) {
+    const int shift = __builtin_ctz(bs);
+    blk = slot >> shift;
+    off = slot & (bs - 1);
+  } else {
+    blk = slot / bs;
+    off = slot - blk * bs;
+  }
   const int64_t dst_base = static_cast<int64_t>(blk) * p.blk_stride + static_cast<int64_t>(off) * p.slot_stride;
-  const int chunks_per_tensor = p.num_kv_heads * kChunksPerHead;
+  const int chunks_per_tensor = p.num_kv_heads * (HEAD_DIM / 8);
   const int total = 2 * chunks_per_tensor;
   const uint4* key_row = p.key + static_cast<int64_t>(tok) * p.key_tok_stride;
   const uint4* value_row = p.value + static_cast<int64_t>(tok) * p.value_tok_stride;
+  uint4* k_dst = p.k_cache + dst_base;
+  uint4* v_dst = p.v_cache + dst_base;
 
   for (int j0 = 0; j0 < total; j0 += 64 * kAppendUnroll) {
-    uint4 buf[kAppendUnroll];
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      const int j = j0 + 64 * u + lane;
-      if (j < total) {
-        const bool is_v = j >= chunks_per_tensor;
-        const int jj = is_v ? j - chunks_per_tensor : j;
-        const int head = jj / kChunksPerHead;
-        const int part = jj - head * kChunksPerHead;
-        const uint4* src = is_v ? value_row + head * p.value_head_stride + part
-                                : key_row + head * p.key_head_stride + part;
-        buf[u] = *src;
-      }
+    // All loads of this group first (addresses clamped to a valid chunk, so no branch
+    // guards the loads and they stay in flight together), then the guarded stores.
+    uint4 b0, b1, b2, b3;
+    int64_t d0, d1, d2, d3;
+    bool v0, v1, v2, v3;
+    {
+      int64_t s0, s1, s2, s3;
+      chunk_offsets<HEAD_DIM>(p, min(j0 + lane, total - 1), chunks_per_tensor, v0, s0, d0);
+      chunk_offsets<HEAD_DIM>(p, min(j0 + 64 + lane, total - 1), chunks_per_tensor, v1, s1, d1);
+      chunk_offsets<HEAD_DIM>(p, min(j0 + 128 + lane, total - 1), chunks_per_tensor, v2, s2, d2);
+      chunk_offsets<HEAD_DIM>(p, min(j0 + 192 + lane, total - 1), chunks_per_tensor, v3, s3, d3);
+      b0 = (v0 ? value_row : key_row)[s0];
+      b1 = (v1 ? value_row : key_row)[s1];
+      b2 = (v2 ? value_row : key_row)[s2];
+      b3 = (v3 ? value_row : key_row)[s3];
     }
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      const int j = j0 + 64 * u + lane;
-      if (j < total) {
-        const bool is_v = j >= chunks_per_tensor;
-        const int jj = is_v ? j - chunks_per_tensor : j;
-        const int head = jj / kChunksPerHead;
-        const int part = jj - head * kChunksPerHead;
-        uint4* dst = (is_v ? p.v_cache : p.k_cache) + dst_base + head * p.head_stride + part;
-        *dst = buf[u];
-      }
-    }
+    if (j0 + lane < total) (v0 ? v_dst : k_dst)[d0] = b0;
+    if (j0 + 64 + lane < total) (v1 ? v_dst : k_dst)[d1] = b1;
+    if (j0 + 128 + lane < total) (v2 ? v_dst : k_dst)[d2] = b2;
+    if (j0 + 192 + lane < total) (v3 ? v_dst : k_dst)[d3] = b3;
   }
 }
 

@@ -4,35 +4,50 @@
 // block_table, softmax_scale, causal=True) as used at
 // kavor/layers/attention/flash_attention_kvcache.py:80-83.
 //
-// Work decomposition (HBM-bound: every KV byte is read exactly once)
-//   grid = (num_splits, num_kv_heads, num_seqs); a workgroup owns one (sequence,
-//   kv head, split) and all G = num_q_heads / num_kv_heads query heads of that kv
-//   head, so GQA costs no extra KV traffic.  A split is `blocks_per_split` logical
-//   blocks; workgroups past a sequence's last block exit at once.
-//   Inside a workgroup the 4 waves walk the split in chunks of 128 tokens, wave w
-//   taking tokens [32w, 32w+32) of the chunk.  Lane (r = lane/16, c = lane%16) owns
-//   dims [8c, 8c+8) of tokens 4i+r, i = 0..7: 8 dwordx4 loads of K and 8 of V per
-//   lane (8 KiB per wave in flight), each 16-lane row reading one 256-byte head row.
+// Work decomposition (HBM-bound: every KV byte is read exactly once) -- stream-K
+//   Work is counted in steps of 16 tokens of one sequence; the steps of all sequences
+//   are laid end to end (prefix sums of ceil(ctx / 16), built in LDS by every
+//   workgroup from context_lens).  The kernel is persistent: its grid is the number of
+//   workgroups the GPU holds at once, independent of the batch and of the block-table
+//   width, so a captured graph never launches empty workgroups.  A workgroup is 4
+//   waves = 4 kv heads; ceil(Hkv / 4) consecutive workgroups form a group that walks
+//   one contiguous range of steps for all kv heads (kv heads of one token row share HBM
+//   pages and are fetched together).  Every group gets the same number of steps
+//   (exact balance whatever the context lengths), at least 16 steps (256 tokens).
+//   A wave owns all G = Hq / Hkv query heads of its kv head, so GQA costs no extra KV
+//   traffic.  Lane (r = lane/16, c = lane%16) owns dims [8c, 8c+8) of tokens 4i+r of a
+//   step (i = 0..3): 4 dwordx4 loads of K and 4 of V per lane, each 16-lane row
+//   reading one 256-byte head row.  The loads of step n+1 are issued before step n is
+//   computed (register double buffer), so 8-16 KiB per wave stay in flight; addresses
+//   past the context are clamped onto its last token (masked in the softmax), so no
+//   branch guards a load.
 //   Scores: q.k with v_dot2c_f32_bf16 on packed bf16 pairs, then a 4-step DPP sum
 //   across the 16-lane row.  Softmax: online, base 2, scale*log2(e) folded into the
-//   scores, one running (max, sum, acc[8]) per lane row.  The 16 row states of a
-//   workgroup (4 rows x 4 waves) are merged through LDS.
-//   Output: a sequence that fits one split writes bf16 directly; otherwise each split
-//   writes (max, sum, unnormalised acc) in fp32 to the workspace and
-//   decode_merge_kernel combines the splits with the same online-softmax rule.
+//   scores, one running (max, sum, acc[8]) per lane row.
+//   Output: where a wave's range ends or a sequence ends, the 4 lane rows are merged
+//   with cross-lane shuffles; a sequence covered by one range writes bf16 directly,
+//   otherwise each range writes (max, sum, unnormalised acc) in fp32 to the workspace
+//   and decode_merge_kernel combines them with the same online-softmax rule.  Partial
+//   traffic is about 2 states per group per sequence boundary: well under 1% of the KV
+//   bytes.
 #include <math.h>
 #include <stdlib.h>
+
+#include <algorithm>
+#include <atomic>
 
 #include "common.h"
 
 namespace kvp {
 
 constexpr int kDecodeHeadDim = 128;
-constexpr int kDecodeWaves = 4;
-constexpr int kWaveTokens = 32;
-constexpr int kLoadsPerLane = kWaveTokens / 4;
-constexpr int kChunkTokens = kDecodeWaves * kWaveTokens;
-constexpr int kRowStates = kDecodeWaves * 4;
+constexpr int kDecodeWaves = 4;  // kv heads per workgroup
+constexpr int kDecodeThreads = 64 * kDecodeWaves;
+constexpr int kStepTokens = 16;
+constexpr int kStepLoads = kStepTokens / 4;  // dwordx4 loads per lane per tensor per step
+constexpr int kMinStepsPerRange = 16;        // a range covers at least 256 tokens
+constexpr int kMaxSeqsPerLaunch = 4096;      // size of the LDS prefix-sum table
+constexpr int kHeaderInts = 16;              // workspace header before the prefix table
 
 struct DecodeParams {
   const uint16_t* q;
@@ -44,69 +59,268 @@ struct DecodeParams {
   const int32_t* block_tables;
   int64_t bt_stride;
   const int32_t* context_lens;
+  int32_t num_seqs;  // <= kMaxSeqsPerLaunch
   int32_t num_q_heads;
+  int32_t num_kv_heads;
   int32_t block_size;
   int32_t max_blocks;
-  int32_t blocks_per_split;
-  int32_t num_splits;
-  float scale_log2;  // softmax_scale * log2(e)
+  int32_t max_parts;  // partial states per (sequence, query head) the workspace holds
+  float scale_log2;   // softmax_scale * log2(e)
   uint16_t* out;
   int64_t o_seq_stride, o_head_stride;
-  float* part_o;   // [num_seqs][num_q_heads][num_splits][128]
-  float* part_ml;  // [num_seqs][num_q_heads][num_splits][2] = (max, sum)
+  int32_t* header;  // [0] steps per range, [kHeaderInts ..] step prefix sums (B + 1)
+  float* part_o;    // [num_seqs][num_q_heads][max_parts][128]
+  float* part_ml;   // [num_seqs][num_q_heads][max_parts][2] = (max, sum)
 };
 
 __device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
   return *reinterpret_cast<const uint4*>(ptr);
 }
 
-template <int G>
-__global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(const DecodeParams p) {
-  constexpr int D = kDecodeHeadDim;
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+// Steps of a sequence; 0 for empty or impossible contexts (written separately).
+__device__ __forceinline__ int seq_steps(int ctx, const DecodeParams& p) {
+  if (ctx <= 0 || ctx > p.max_blocks * p.block_size) return 0;
+  return (ctx + kStepTokens - 1) / kStepTokens;
+}
+
+// s_cum[b] = steps of sequences 0..b-1 (b = 0..num_seqs), built by the whole workgroup:
+// each thread sums a contiguous run of sequences, then a Hillis-Steele scan over the
+// 256 run totals.
+__device__ void build_step_prefix(const DecodeParams& p, int* s_cum, int* s_part) {
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int B = p.num_seqs;
+  const int per = (B + kDecodeThreads - 1) / kDecodeThreads;
+  const int j0 = tid * per;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int b = j0 + i;
+    if (b < B) local += seq_steps(p.context_lens[b], p);
+  }
+  s_part[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < kDecodeThreads; off <<= 1) {
+    const int v = tid >= off ? s_part[tid - off] : 0;
+    __syncthreads();
+    s_part[tid] += v;
+    __syncthreads();
+  }
+  int run = s_part[tid] - local;
+  for (int i = 0; i < per; ++i) {
+    const int b = j0 + i;
+    if (b < B) {
+      s_cum[b] = run;
+      run += seq_steps(p.context_lens[b], p);
+    }
+  }
+  if (tid == kDecodeThreads - 1) s_cum[B] = s_part[tid];
+  __syncthreads();
+}
+
+// Ranges [part_first(b), part_last(b)] touch sequence b's steps [cum_b, cum_b1).
+__device__ __forceinline__ int num_parts(int cum_b, int cum_b1, int spr) {
+  return (cum_b1 - 1) / spr - cum_b / spr + 1;
+}
+
+// Per-wave cursor over the steps of one range.
+struct StepCursor {
+  int b;        // sequence
+  int j;        // step within the sequence
+  int nsteps;   // steps of sequence b
+  int ctx;      // context length of sequence b
+  int lblk;     // logical block whose id is cached in blk (-1: none)
+  int blk;      // physical block id of lblk
+  int pf_blk;   // id of block lblk + 1, loaded one block ahead (-1: not loaded)
+  bool bad;     // a needed block id was out of range
+};
+
+__device__ __forceinline__ void cursor_start_seq(const DecodeParams& p, StepCursor& cur, int b, int j) {
+  cur.b = b;
+  cur.j = j;
+  cur.ctx = p.context_lens[b];
+  cur.nsteps = seq_steps(cur.ctx, p);
+  cur.lblk = -1;
+  cur.blk = 0;
+  cur.pf_blk = -1;
+  cur.bad = false;
+}
+
+// Address (in elements) of this lane's first token of the cursor's step, and the number
+// of valid tokens of the step.  On entering a block it takes the id prefetched one
+// block earlier (or loads it) and prefetches the next block's id, so the scalar load
+// is off the critical path.
+__device__ __forceinline__ int64_t step_base(const DecodeParams& p, StepCursor& cur, int64_t head_off,
+                                            int& nvalid) {
+  const int t0 = cur.j * kStepTokens;
+  const int lblk = t0 / p.block_size;
+  if (lblk != cur.lblk) {
+    const int32_t* row = p.block_tables + cur.b * p.bt_stride;
+    int blk = (cur.lblk >= 0 && lblk == cur.lblk + 1 && cur.pf_blk != -1) ? cur.pf_blk : row[lblk];
+    if (blk < 0 || blk >= p.num_cache_blocks) {
+      cur.bad = true;
+      blk = 0;
+    }
+    cur.blk = blk;
+    cur.lblk = lblk;
+    cur.pf_blk = (lblk + 1) * p.block_size < cur.ctx ? row[lblk + 1] : -1;
+  }
+  nvalid = min(kStepTokens, cur.ctx - t0);
+  return static_cast<int64_t>(cur.blk) * p.blk_stride +
+         static_cast<int64_t>(t0 - lblk * p.block_size) * p.slot_stride + head_off;
+}
+
+// Token 4i + r of the step, clamped onto the last valid token so every load is in
+// bounds and needs no branch; clamped tokens are masked out of the softmax.
+__device__ __forceinline__ void step_load(const DecodeParams& p, int64_t base, int nvalid, int r,
+                                          uint4 (&kr)[kStepLoads], uint4 (&vr)[kStepLoads]) {
+#pragma unroll
+  for (int i = 0; i < kStepLoads; ++i) {
+    const int t = min(4 * i + r, nvalid - 1);
+    kr[i] = load16(p.k_cache + base + t * p.slot_stride);
+    vr[i] = load16(p.v_cache + base + t * p.slot_stride);
+  }
+}
+
+template <int G>
+__device__ __forceinline__ void step_compute(const DecodeParams& p, const uint4 (&qv)[G],
+                                             const uint4 (&kr)[kStepLoads], const uint4 (&vr)[kStepLoads],
+                                             int nvalid, int r, float (&m)[G], float (&l)[G],
+                                             float (&acc)[G][8]) {
+  float s[G][kStepLoads];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mx = kMaxFloor;
+#pragma unroll
+    for (int i = 0; i < kStepLoads; ++i) {
+      float part = dot2_bf16(qv[g].x, kr[i].x, 0.f);
+      part = dot2_bf16(qv[g].y, kr[i].y, part);
+      part = dot2_bf16(qv[g].z, kr[i].z, part);
+      part = dot2_bf16(qv[g].w, kr[i].w, part);
+      const float sc = row16_sum(part) * p.scale_log2;
+      s[g][i] = (4 * i + r < nvalid) ? sc : -INFINITY;
+      mx = fmaxf(mx, s[g][i]);
+    }
+    const float m_new = fmaxf(m[g], mx);
+    const float alpha = fast_exp2(m[g] - m_new);
+    m[g] = m_new;
+    l[g] *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
+  }
+  // P V: each V row is widened to fp32 once and feeds all G heads.
+#pragma unroll
+  for (int i = 0; i < kStepLoads; ++i) {
+    const float vf[8] = {bf16_lo(vr[i].x), bf16_hi(vr[i].x), bf16_lo(vr[i].y), bf16_hi(vr[i].y),
+                         bf16_lo(vr[i].z), bf16_hi(vr[i].z), bf16_lo(vr[i].w), bf16_hi(vr[i].w)};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float pr = fast_exp2(s[g][i] - m[g]);
+      l[g] += pr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] += pr * vf[j];
+    }
+  }
+}
+
+// Merges the 4 lane rows of the wave and writes the state of (b, kvh) for this range:
+// the bf16 output when one range covers the sequence, otherwise an fp32 partial.
+template <int G>
+__device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh, int part, bool single,
+                                           bool bad, int lane, float (&m)[G], float (&l)[G],
+                                           float (&acc)[G][8]) {
+  const int c = lane & 15;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mm = fmaxf(m[g], __shfl_xor(m[g], 16));
+    mm = fmaxf(mm, __shfl_xor(mm, 32));
+    const float sc = fast_exp2(m[g] - mm);
+    float ll = l[g] * sc;
+    ll += __shfl_xor(ll, 16);
+    ll += __shfl_xor(ll, 32);
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[j] = acc[g][j] * sc;
+      a[j] += __shfl_xor(a[j], 16);
+      a[j] += __shfl_xor(a[j], 32);
+    }
+    if (bad) ll = NAN;
+    const int h = kvh * G + g;
+    if (lane < 16) {
+      if (single) {
+        const float inv = 1.f / ll;
+        uint4 o;
+        o.x = pack_bf16x2(a[0] * inv, a[1] * inv);
+        o.y = pack_bf16x2(a[2] * inv, a[3] * inv);
+        o.z = pack_bf16x2(a[4] * inv, a[5] * inv);
+        o.w = pack_bf16x2(a[6] * inv, a[7] * inv);
+        *reinterpret_cast<uint4*>(p.out + b * p.o_seq_stride + h * p.o_head_stride + 8 * c) = o;
+      } else {
+        const int64_t row = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.max_parts + part;
+        float4* dst = reinterpret_cast<float4*>(p.part_o + row * kDecodeHeadDim + 8 * c);
+        dst[0] = make_float4(a[0], a[1], a[2], a[3]);
+        dst[1] = make_float4(a[4], a[5], a[6], a[7]);
+        if (c == 0) *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(mm, ll);
+      }
+    }
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const DecodeParams p) {
+  constexpr int D = kDecodeHeadDim;
+  __shared__ int s_cum[kMaxSeqsPerLaunch + 1];
+  __shared__ int s_part[kDecodeThreads];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r = lane >> 4;
   const int c = lane & 15;
 
-  const int bs = p.block_size;
-  const int ctx = p.context_lens[b];
-  const int capacity = p.max_blocks * bs;
-  if (ctx <= 0 || ctx > capacity) {
-    // Empty (graph padding) rows read as zeros; impossible lengths read as NaN.
-    if (split == 0) {
-      const uint16_t fill = ctx <= 0 ? 0 : 0x7fc0;
-      for (int o = tid; o < G * D; o += 64 * kDecodeWaves) {
-        const int g = o / D, d = o - g * D;
-        p.out[b * p.o_seq_stride + (kvh * G + g) * p.o_head_stride + d] = fill;
-      }
+  // Rows with nothing to attend (ctx 0: graph padding) read as zeros; impossible
+  // lengths read as NaN.  Neither has steps.
+  for (int b = blockIdx.x; b < p.num_seqs; b += gridDim.x) {
+    const int ctx = p.context_lens[b];
+    if (ctx > 0 && ctx <= p.max_blocks * p.block_size) continue;
+    const uint16_t fill = ctx <= 0 ? 0 : 0x7fc0;
+    for (int o = tid; o < p.num_q_heads * D; o += kDecodeThreads) {
+      const int h = o / D, d = o - h * D;
+      p.out[b * p.o_seq_stride + h * p.o_head_stride + d] = fill;
     }
-    return;
   }
-  const int nblk = (ctx + bs - 1) / bs;
-  const int bps = p.blocks_per_split;
-  const int blk_begin = split * bps;
-  if (blk_begin >= nblk) return;
-  const int blk_end = min(nblk, blk_begin + bps);
-  const int nsplit_seq = (nblk + bps - 1) / bps;
-  const int tok_begin = blk_begin * bs;
-  const int tok_end = min(ctx, blk_end * bs);
 
-  __shared__ int s_bad;
-  __shared__ float s_m[G][kRowStates];
-  __shared__ float s_l[G][kRowStates];
-  __shared__ float s_acc[G][kRowStates][D];
-  if (tid == 0) s_bad = 0;
+  build_step_prefix(p, s_cum, s_part);
+  const int B = p.num_seqs;
+  const int total_steps = s_cum[B];
+  const int groups_per_range = (p.num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
+  const int num_ranges = max(1, static_cast<int>(gridDim.x) / groups_per_range);
+  const int spr = max(kMinStepsPerRange, (total_steps + num_ranges - 1) / num_ranges);
+  if (blockIdx.x == 0) {  // for the merge kernel
+    if (tid == 0) p.header[0] = spr;
+    for (int b = tid; b <= B; b += kDecodeThreads) p.header[kHeaderInts + b] = s_cum[b];
+  }
 
-  // This lane's query slice: dims [8c, 8c+8) of every query head of the group.
+  const int range = blockIdx.x / groups_per_range;
+  const int kvh = (blockIdx.x - range * groups_per_range) * kDecodeWaves + wave;
+  const int S0 = range * spr;
+  const int S1 = min(total_steps, S0 + spr);
+  if (kvh >= p.num_kv_heads || S0 >= S1) return;  // no barrier follows
+
+  // Sequence holding step S0: s_cum[b] <= S0 < s_cum[b + 1].
+  int lo = 0, hi = B;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (s_cum[mid] <= S0) lo = mid;
+    else hi = mid;
+  }
+  StepCursor cur;
+  cursor_start_seq(p, cur, lo, S0 - s_cum[lo]);
+  const int64_t head_off = static_cast<int64_t>(kvh) * p.head_stride + 8 * c;
+
   uint4 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    qv[g] = load16(p.q + b * p.q_seq_stride + (kvh * G + g) * p.q_head_stride + 8 * c);
-
+    qv[g] = load16(p.q + cur.b * p.q_seq_stride + (kvh * G + g) * p.q_head_stride + 8 * c);
   float m[G], l[G], acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -116,136 +330,76 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(const D
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
   }
 
-  const int32_t* bt_row = p.block_tables + b * p.bt_stride;
-  const int64_t head_off = static_cast<int64_t>(kvh) * p.head_stride + 8 * c;
-  bool bad = false;
+  uint4 kA[kStepLoads], vA[kStepLoads], kB[kStepLoads], vB[kStepLoads];
+  int nvA, nvB = 0;
+  step_load(p, step_base(p, cur, head_off, nvA), nvA, r, kA, vA);
 
-  for (int t0 = tok_begin; t0 < tok_end; t0 += kChunkTokens) {
-    const int tw = t0 + kWaveTokens * wave;  // first token of this wave's slice
-    if (tw >= tok_end) continue;             // wave-uniform
-    const int lblk = tw / bs;
-    int blk = bt_row[lblk];
-    if (blk < 0 || blk >= p.num_cache_blocks) {
-      bad = true;
-      blk = 0;
-    }
-    const int64_t base = static_cast<int64_t>(blk) * p.blk_stride +
-                         static_cast<int64_t>(tw - lblk * bs) * p.slot_stride + head_off;
-    const int nvalid = tok_end - tw;  // tokens of this wave's slice that exist (may exceed it)
-
-    uint4 kr[kLoadsPerLane], vr[kLoadsPerLane];
+  // One step: prefetch the next step into (kN, vN), compute (kC, vC), emit at the end
+  // of a sequence or of the range.  Returns false when the range is done.
+  auto advance = [&](uint4 (&kC)[kStepLoads], uint4 (&vC)[kStepLoads], int nvC,
+                     uint4 (&kN)[kStepLoads], uint4 (&vN)[kStepLoads], int& nvN, int S) -> bool {
+    const bool more = S + 1 < S1;
+    const bool seq_end = cur.j + 1 == cur.nsteps;
+    StepCursor nxt = cur;
+    uint4 qn[G];
+    if (more) {
+      if (seq_end) {
+        // next non-empty sequence: the one whose steps start at S + 1
+        int nb = cur.b + 1;
+        while (s_cum[nb + 1] == S + 1) ++nb;
+        cursor_start_seq(p, nxt, nb, 0);
 #pragma unroll
-    for (int i = 0; i < kLoadsPerLane; ++i) {
-      const int t = 4 * i + r;
-      kr[i] = make_uint4(0, 0, 0, 0);
-      if (t < nvalid) kr[i] = load16(p.k_cache + base + t * p.slot_stride);
-    }
-#pragma unroll
-    for (int i = 0; i < kLoadsPerLane; ++i) {
-      const int t = 4 * i + r;
-      vr[i] = make_uint4(0, 0, 0, 0);
-      if (t < nvalid) vr[i] = load16(p.v_cache + base + t * p.slot_stride);
-    }
-
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float s[kLoadsPerLane];
-      float mx = kMaxFloor;
-#pragma unroll
-      for (int i = 0; i < kLoadsPerLane; ++i) {
-        float part = dot2_bf16(qv[g].x, kr[i].x, 0.f);
-        part = dot2_bf16(qv[g].y, kr[i].y, part);
-        part = dot2_bf16(qv[g].z, kr[i].z, part);
-        part = dot2_bf16(qv[g].w, kr[i].w, part);
-        const float sc = row16_sum(part) * p.scale_log2;
-        s[i] = (4 * i + r < nvalid) ? sc : -INFINITY;
-        mx = fmaxf(mx, s[i]);
+        for (int g = 0; g < G; ++g)
+          qn[g] = load16(p.q + nb * p.q_seq_stride + (kvh * G + g) * p.q_head_stride + 8 * c);
+      } else {
+        nxt.j = cur.j + 1;
       }
-      const float m_new = fmaxf(m[g], mx);
-      const float alpha = fast_exp2(m[g] - m_new);
-      m[g] = m_new;
-      float lsum = l[g] * alpha;
+      step_load(p, step_base(p, nxt, head_off, nvN), nvN, r, kN, vN);
+    }
+    step_compute<G>(p, qv, kC, vC, nvC, r, m, l, acc);
+    if (seq_end || !more) {
+      const int cb = s_cum[cur.b], cb1 = s_cum[cur.b + 1];
+      const int np = num_parts(cb, cb1, spr);
+      emit_state<G>(p, cur.b, kvh, range - cb / spr, np == 1, cur.bad, lane, m, l, acc);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
+      for (int g = 0; g < G; ++g) {
+        m[g] = kMaxFloor;
+        l[g] = 0.f;
 #pragma unroll
-      for (int i = 0; i < kLoadsPerLane; ++i) {
-        const float pr = fast_exp2(s[i] - m_new);
-        lsum += pr;
-        acc[g][0] += pr * bf16_lo(vr[i].x);
-        acc[g][1] += pr * bf16_hi(vr[i].x);
-        acc[g][2] += pr * bf16_lo(vr[i].y);
-        acc[g][3] += pr * bf16_hi(vr[i].y);
-        acc[g][4] += pr * bf16_lo(vr[i].z);
-        acc[g][5] += pr * bf16_hi(vr[i].z);
-        acc[g][6] += pr * bf16_lo(vr[i].w);
-        acc[g][7] += pr * bf16_hi(vr[i].w);
+        for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
       }
-      l[g] = lsum;
-    }
-  }
-
-  __syncthreads();  // s_bad initialised before any wave may set it
-  if (bad) s_bad = 1;
-  const int rs = wave * 4 + r;
+      if (more) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (c == 0) {
-      s_m[g][rs] = m[g];
-      s_l[g][rs] = l[g];
-    }
-    float4* dst = reinterpret_cast<float4*>(&s_acc[g][rs][8 * c]);
-    dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-    dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-  }
-  __syncthreads();
-
-  const bool poisoned = s_bad != 0;
-  for (int o = tid; o < G * D; o += 64 * kDecodeWaves) {
-    const int g = o / D, d = o - g * D;
-    float mm = kMaxFloor;
-#pragma unroll
-    for (int k = 0; k < kRowStates; ++k) mm = fmaxf(mm, s_m[g][k]);
-    float ll = 0.f, oo = 0.f;
-#pragma unroll
-    for (int k = 0; k < kRowStates; ++k) {
-      const float w = fast_exp2(s_m[g][k] - mm);
-      ll += w * s_l[g][k];
-      oo += w * s_acc[g][k][d];
-    }
-    if (poisoned) ll = NAN;
-    const int h = kvh * G + g;
-    if (nsplit_seq == 1) {
-      p.out[b * p.o_seq_stride + h * p.o_head_stride + d] = f32_to_bf16(oo / ll);
-    } else {
-      const int64_t row = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.num_splits + split;
-      p.part_o[row * D + d] = oo;
-      if (d == 0) {
-        p.part_ml[row * 2] = mm;
-        p.part_ml[row * 2 + 1] = ll;
+        for (int g = 0; g < G; ++g) qv[g] = qn[g];
       }
     }
+    cur = nxt;
+    return more;
+  };
+
+  for (int S = S0;; S += 2) {
+    if (!advance(kA, vA, nvA, kB, vB, nvB, S)) break;
+    if (!advance(kB, vB, nvB, kA, vA, nvA, S + 1)) break;
   }
 }
 
-// Combines the per-split partial states of sequences that span several splits.
+// Combines the per-range partial states of sequences that span several ranges.
 // grid = (num_q_heads, num_seqs), 128 threads (one per head dim).
 __global__ __launch_bounds__(kDecodeHeadDim) void decode_merge_kernel(const DecodeParams p) {
   constexpr int D = kDecodeHeadDim;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
-  const int bs = p.block_size;
-  const int ctx = p.context_lens[b];
-  if (ctx <= 0 || ctx > p.max_blocks * bs) return;
-  const int nblk = (ctx + bs - 1) / bs;
-  const int ns = (nblk + p.blocks_per_split - 1) / p.blocks_per_split;
-  if (ns <= 1) return;
-  const int64_t row0 = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.num_splits;
+  const int cb = p.header[kHeaderInts + b], cb1 = p.header[kHeaderInts + b + 1];
+  if (cb1 <= cb) return;  // no steps: written by the main kernel
+  const int np = num_parts(cb, cb1, p.header[0]);
+  if (np <= 1) return;
+  const int64_t row0 = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.max_parts;
   const float* ml = p.part_ml + row0 * 2;
   float mm = kMaxFloor;
-  for (int s = 0; s < ns; ++s) mm = fmaxf(mm, ml[2 * s]);
+  for (int s = 0; s < np; ++s) mm = fmaxf(mm, ml[2 * s]);
   float ll = 0.f, oo = 0.f;
-  for (int s = 0; s < ns; ++s) {
+  for (int s = 0; s < np; ++s) {
     const float w = fast_exp2(ml[2 * s] - mm);
     ll += w * ml[2 * s + 1];
     oo += w * p.part_o[(row0 + s) * D + d];
@@ -253,28 +407,65 @@ __global__ __launch_bounds__(kDecodeHeadDim) void decode_merge_kernel(const Deco
   p.out[b * p.o_seq_stride + h * p.o_head_stride + d] = f32_to_bf16(oo / ll);
 }
 
-// Blocks per split: one 256-token block per workgroup keeps ragged batches balanced;
-// very wide block tables group blocks so that no sequence needs more than 32 splits,
-// which bounds the fp32 partial traffic to well under 2% of the KV bytes.
-static int choose_blocks_per_split(int max_blocks) {
-  static int forced = [] {
-    const char* env = getenv("KVP_DECODE_BLOCKS_PER_SPLIT");
+// Partial states per (sequence, query head): a sequence of at most max_tokens tokens
+// spans at most ceil(steps / kMinStepsPerRange) + 1 ranges.
+static int64_t decode_max_parts(int64_t max_blocks, int64_t block_size) {
+  const int64_t steps = (max_blocks * block_size + kStepTokens - 1) / kStepTokens;
+  return (steps + kMinStepsPerRange - 1) / kMinStepsPerRange + 1;
+}
+
+static int64_t decode_workspace_need(int64_t seqs, int64_t q_heads, int64_t max_parts) {
+  const int64_t header = (kHeaderInts + kMaxSeqsPerLaunch + 1) * 4;
+  const int64_t header_padded = (header + 255) / 256 * 256;
+  return header_padded + seqs * q_heads * max_parts * (kDecodeHeadDim + 2) * 4;
+}
+
+// Workgroups of paged_decode_kernel<G> resident on the whole current device.
+template <int G>
+static int resident_workgroups() {
+  static std::atomic<int> cached[16];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<G>, kDecodeThreads, 0) !=
+          hipSuccess || per_cu <= 0)
+    per_cu = 1;
+  v = cus * per_cu;
+  cached[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+template <int G>
+static void launch_decode(const DecodeParams& p, int64_t max_steps, hipStream_t s) {
+  static const int forced = [] {
+    const char* env = getenv("KVP_DECODE_GRID");
     return env ? atoi(env) : 0;
   }();
-  if (forced > 0) return forced;
-  return max_blocks <= 32 ? 1 : (max_blocks + 31) / 32;
+  const int64_t groups_per_range = (p.num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
+  const int64_t grid0 = forced > 0 ? forced : resident_workgroups<G>();
+  // no more ranges than minimum-size ranges over the largest possible work
+  const int64_t max_ranges = std::max<int64_t>(1, (max_steps + kMinStepsPerRange - 1) / kMinStepsPerRange);
+  const int64_t ranges = std::max<int64_t>(1, std::min<int64_t>(grid0 / groups_per_range, max_ranges));
+  const int64_t grid = ranges * groups_per_range;
+  hipLaunchKernelGGL(paged_decode_kernel<G>, dim3(static_cast<unsigned>(grid)), dim3(kDecodeThreads), 0, s, p);
 }
 
 }  // namespace kvp
 
 using namespace kvp;
 
-extern "C" size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q_heads,
-                                             int32_t head_dim, int32_t max_blocks_per_seq) {
-  if (max_num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0) return 0;
-  // Sized for one block per split, the finest split choose_blocks_per_split can make.
-  return static_cast<size_t>(max_num_seqs) * num_q_heads * max_blocks_per_seq *
-         (static_cast<size_t>(head_dim) + 2) * sizeof(float);
+extern "C" size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q_heads, int32_t head_dim,
+                                             int32_t max_blocks_per_seq, int32_t block_size) {
+  if (max_num_seqs <= 0 || num_q_heads <= 0 || head_dim != kDecodeHeadDim || max_blocks_per_seq <= 0 ||
+      block_size <= 0)
+    return 0;
+  const int64_t seqs = std::min<int64_t>(max_num_seqs, kMaxSeqsPerLaunch);
+  return static_cast<size_t>(
+      decode_workspace_need(seqs, num_q_heads, decode_max_parts(max_blocks_per_seq, block_size)));
 }
 
 extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
@@ -291,14 +482,11 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
   clear_error();
   if (num_seqs < 0) return fail(KVP_EINVAL, "kvp_paged_decode_bf16: num_seqs=%d < 0", num_seqs);
   if (num_seqs == 0) return KVP_OK;
-  if (num_seqs > 65535) return fail(KVP_EINVAL, "kvp_paged_decode_bf16: num_seqs=%d > 65535", num_seqs);
   if (head_dim != kDecodeHeadDim)
     return fail(KVP_EUNSUPPORTED, "kvp_paged_decode_bf16: head_dim=%d (supported: 128)", head_dim);
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
     return fail(KVP_EINVAL, "kvp_paged_decode_bf16: num_q_heads=%d not a multiple of num_kv_heads=%d",
                 num_q_heads, num_kv_heads);
-  if (num_kv_heads > 65535)
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: num_kv_heads=%d > 65535", num_kv_heads);
   const int G = num_q_heads / num_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(KVP_EUNSUPPORTED, "kvp_paged_decode_bf16: GQA ratio %d (supported: 1, 2, 4, 8)", G);
@@ -324,56 +512,62 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
       !mult8(cache_slot_stride) || !mult8(cache_head_stride))
     return fail(KVP_EINVAL, "kvp_paged_decode_bf16: q and cache strides must be multiples of 8 elements");
 
-  const int bps = choose_blocks_per_split(max_blocks_per_seq);
-  const int num_splits = (max_blocks_per_seq + bps - 1) / bps;
-  const size_t need = static_cast<size_t>(num_seqs) * num_q_heads * num_splits *
-                      (kDecodeHeadDim + 2) * sizeof(float);
-  if (num_splits > 1) {
-    if (!workspace || workspace_bytes < need)
-      return fail(KVP_EWORKSPACE, "kvp_paged_decode_bf16: workspace of %zu bytes, %zu needed",
-                  workspace_bytes, need);
-    if (reinterpret_cast<uintptr_t>(workspace) & 15u)
-      return fail(KVP_EINVAL, "kvp_paged_decode_bf16: workspace must be 16-byte aligned");
-  }
-
-  DecodeParams p;
-  p.q = static_cast<const uint16_t*>(q);
-  p.q_seq_stride = q_seq_stride;
-  p.q_head_stride = q_head_stride;
-  p.k_cache = static_cast<const uint16_t*>(k_cache);
-  p.v_cache = static_cast<const uint16_t*>(v_cache);
-  p.blk_stride = cache_block_stride;
-  p.slot_stride = cache_slot_stride;
-  p.head_stride = cache_head_stride;
-  p.num_cache_blocks = num_cache_blocks;
-  p.block_tables = block_tables;
-  p.bt_stride = block_table_stride;
-  p.context_lens = context_lens;
-  p.num_q_heads = num_q_heads;
-  p.block_size = block_size;
-  p.max_blocks = max_blocks_per_seq;
-  p.blocks_per_split = bps;
-  p.num_splits = num_splits;
-  p.scale_log2 = softmax_scale * 1.4426950408889634f;
-  p.out = static_cast<uint16_t*>(out);
-  p.o_seq_stride = out_seq_stride;
-  p.o_head_stride = out_head_stride;
-  float* ws = static_cast<float*>(workspace);
-  p.part_o = ws;
-  p.part_ml = ws ? ws + static_cast<size_t>(num_seqs) * num_q_heads * num_splits * kDecodeHeadDim
-                 : nullptr;
+  const int chunk_seqs = std::min(num_seqs, kMaxSeqsPerLaunch);
+  const int64_t max_parts = decode_max_parts(max_blocks_per_seq, block_size);
+  const size_t need = static_cast<size_t>(decode_workspace_need(chunk_seqs, num_q_heads, max_parts));
+  if (!workspace || workspace_bytes < need)
+    return fail(KVP_EWORKSPACE, "kvp_paged_decode_bf16: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: workspace must be 256-byte aligned");
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(num_splits, num_kv_heads, num_seqs);
-  const dim3 block(64 * kDecodeWaves);
-  switch (G) {
-    case 1: hipLaunchKernelGGL(paged_decode_kernel<1>, grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL(paged_decode_kernel<2>, grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL(paged_decode_kernel<4>, grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL(paged_decode_kernel<8>, grid, block, 0, s, p); break;
+  const int64_t header_bytes = (((kHeaderInts + kMaxSeqsPerLaunch + 1) * 4) + 255) / 256 * 256;
+  const int64_t steps_per_seq = (static_cast<int64_t>(max_blocks_per_seq) * block_size + kStepTokens - 1) / kStepTokens;
+  // Batches beyond the LDS prefix table run as consecutive launches of up to 4096
+  // sequences; they reuse the workspace in stream order.
+  for (int b0 = 0; b0 < num_seqs; b0 += kMaxSeqsPerLaunch) {
+    const int nb = std::min(kMaxSeqsPerLaunch, num_seqs - b0);
+    DecodeParams p;
+    p.q = static_cast<const uint16_t*>(q) + b0 * q_seq_stride;
+    p.q_seq_stride = q_seq_stride;
+    p.q_head_stride = q_head_stride;
+    p.k_cache = static_cast<const uint16_t*>(k_cache);
+    p.v_cache = static_cast<const uint16_t*>(v_cache);
+    p.blk_stride = cache_block_stride;
+    p.slot_stride = cache_slot_stride;
+    p.head_stride = cache_head_stride;
+    p.num_cache_blocks = num_cache_blocks;
+    p.block_tables = block_tables + b0 * block_table_stride;
+    p.bt_stride = block_table_stride;
+    p.context_lens = context_lens + b0;
+    p.num_seqs = nb;
+    p.num_q_heads = num_q_heads;
+    p.num_kv_heads = num_kv_heads;
+    p.block_size = block_size;
+    p.max_blocks = max_blocks_per_seq;
+    p.max_parts = static_cast<int32_t>(max_parts);
+    p.scale_log2 = softmax_scale * 1.4426950408889634f;
+    p.out = static_cast<uint16_t*>(out) + b0 * out_seq_stride;
+    p.o_seq_stride = out_seq_stride;
+    p.o_head_stride = out_head_stride;
+    char* ws = static_cast<char*>(workspace);
+    p.header = reinterpret_cast<int32_t*>(ws);
+    p.part_o = reinterpret_cast<float*>(ws + header_bytes);
+    p.part_ml = p.part_o + static_cast<size_t>(nb) * num_q_heads * max_parts * kDecodeHeadDim;
+
+    const int64_t max_steps = static_cast<int64_t>(nb) * steps_per_seq;
+    switch (G) {
+      case 1: launch_decode<1>(p, max_steps, s); break;
+      case 2: launch_decode<2>(p, max_steps, s); break;
+      case 4: launch_decode<4>(p, max_steps, s); break;
+      default: launch_decode<8>(p, max_steps, s); break;
+    }
+    int rc = launch_status("kvp_paged_decode_bf16");
+    if (rc != KVP_OK) return rc;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(num_q_heads, nb), dim3(kDecodeHeadDim), 0, s, p);
+    rc = launch_status("kvp_paged_decode_bf16 (merge)");
+    if (rc != KVP_OK) return rc;
   }
-  int rc = launch_status("kvp_paged_decode_bf16");
-  if (rc != KVP_OK || num_splits == 1) return rc;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(num_q_heads, num_seqs), dim3(kDecodeHeadDim), 0, s, p);
-  return launch_status("kvp_paged_decode_bf16 (merge)");
+  return KVP_OK;
 }

@@ -90,14 +90,16 @@ _workspaces: dict[int, torch.Tensor] = {}
 
 
 def decode_workspace_bytes(max_num_seqs: int, num_q_heads: int, head_dim: int,
-                           max_blocks_per_seq: int) -> int:
-    return int(lib().kvp_decode_workspace_bytes(max_num_seqs, num_q_heads, head_dim, max_blocks_per_seq))
+                           max_blocks_per_seq: int, block_size: int) -> int:
+    return int(lib().kvp_decode_workspace_bytes(max_num_seqs, num_q_heads, head_dim,
+                                                 max_blocks_per_seq, block_size))
 
 
 def reserve_decode_workspace(max_num_seqs: int, num_q_heads: int, head_dim: int,
-                             max_blocks_per_seq: int, device: torch.device | str | int) -> torch.Tensor:
-    """Allocates (or grows) the per-device split-K workspace.  Call before graph capture."""
-    nbytes = decode_workspace_bytes(max_num_seqs, num_q_heads, head_dim, max_blocks_per_seq)
+                             max_blocks_per_seq: int, block_size: int,
+                             device: torch.device | str | int) -> torch.Tensor:
+    """Allocates (or grows) the per-device decode workspace.  Call before graph capture."""
+    nbytes = decode_workspace_bytes(max_num_seqs, num_q_heads, head_dim, max_blocks_per_seq, block_size)
     dev = torch.device(device) if not isinstance(device, int) else torch.device("cuda", device)
     if dev.index is None:
         dev = torch.device("cuda", torch.cuda.current_device())
@@ -154,7 +156,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         if out3.shape != (B, Hq, D) or out3.dtype != torch.bfloat16 or out3.stride(2) != 1:
             raise ValueError("out must be bf16 [B, 1, Hq, D] or [B, Hq, D] with contiguous head_dim")
     max_blocks = block_table.shape[1]
-    ws = reserve_decode_workspace(B, Hq, D, max_blocks, q3.device)
+    ws = reserve_decode_workspace(B, Hq, D, max_blocks, block_size, q3.device)
     rc = lib().kvp_paged_decode_bf16(
         q3.data_ptr(), q3.stride(0), q3.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(),

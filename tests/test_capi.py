@@ -59,7 +59,7 @@ def test_append_rejects_bad_arguments_on_host():
 def _decode(**over):
     args = dict(q=16, qs=2048, qh=128, kc=16, vc=16, bstr=524288, sstr=1024, hstr=128, nblk=64,
                 bt=16, bts=16, ctx=16, b=4, hq=16, hkv=8, d=128, bs=256, maxb=16, scale=0.088,
-                out=16, os=2048, oh=128, ws=16, wsb=1 << 30, stream=None)
+                out=16, os=2048, oh=128, ws=256, wsb=1 << 30, stream=None)
     args.update(over)
     return _lib.lib().kvp_paged_decode_bf16(*args.values())
 
@@ -71,14 +71,20 @@ def test_decode_rejects_bad_arguments_on_host():
     assert _decode(hq=24) == _lib.KVP_EUNSUPPORTED           # GQA ratio 3
     assert _decode(bs=100) == _lib.KVP_EINVAL                # not a multiple of 64
     assert _decode(bts=8) == _lib.KVP_EINVAL                 # table stride < width
-    assert _decode(wsb=100) == _lib.KVP_EWORKSPACE           # 16 splits need partials
+    assert _decode(wsb=100) == _lib.KVP_EWORKSPACE           # smaller than the header
+    assert _decode(ws=32) == _lib.KVP_EINVAL                 # not 256-byte aligned
     assert b"workspace" in _lib.lib().kvp_last_error()
 
 
 def test_decode_workspace_size_formula():
-    # seqs * q heads * max blocks * (head_dim + 2) fp32 values
-    assert _lib.lib().kvp_decode_workspace_bytes(512, 16, 128, 16) == 512 * 16 * 16 * 130 * 4
-    assert _lib.lib().kvp_decode_workspace_bytes(0, 16, 128, 16) == 0
+    # 256-byte-aligned header (16 ints + a 4097-entry prefix table), then per (sequence,
+    # query head) up to ceil(ceil(ctx_max / 16) / 16) + 1 partial states of 130 floats
+    header = ((16 + 4097) * 4 + 255) // 256 * 256
+    parts = -(-(16 * 256 // 16) // 16) + 1
+    assert _lib.lib().kvp_decode_workspace_bytes(512, 16, 128, 16, 256) == header + 512 * 16 * parts * 130 * 4
+    assert _lib.lib().kvp_decode_workspace_bytes(9000, 16, 128, 16, 256) == header + 4096 * 16 * parts * 130 * 4
+    assert _lib.lib().kvp_decode_workspace_bytes(0, 16, 128, 16, 256) == 0
+    assert _lib.lib().kvp_decode_workspace_bytes(8, 16, 64, 16, 256) == 0
 
 
 def _prefill(**over):

@@ -105,18 +105,25 @@ def test_decode_invalid_block_poisons_only_its_sequence(cuda_device):
     assert torch.isnan(out2[0]).all() and not torch.isnan(out2[1:]).any()
 
 
-def test_decode_batch_permutation_is_bitwise_invariant(cuda_device):
+def test_decode_deterministic_and_permutation_consistent(cuda_device):
+    """Repeating a call gives identical bits.  Permuting the batch moves the points where
+    the work split cuts a sequence (the split balances the whole batch), so the permuted
+    outputs agree within tolerance, and both agree with the oracle."""
     q, kc, vc, bt, ctx = _case(15, B=32, hq=16, hkv=8, bs=256, lo=1, hi=2048)
     d = cuda_device
     perm = torch.randperm(32, generator=gen(150))
     a = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt.to(d)).cpu()
+    a2 = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt.to(d)).cpu()
+    assert bits_equal(a, a2)
     b = _decode(q[perm].to(d), kc.to(d), vc.to(d), ctx[perm].to(d), bt[perm].contiguous().to(d)).cpu()
-    assert bits_equal(a[perm], b)
+    torch.testing.assert_close(a[perm].float(), b.float(), **TOL)
+    torch.testing.assert_close(a.float(), ref.paged_decode(q, kc, vc, bt, ctx, SCALE), **TOL)
 
 
-def test_decode_split_granularity_stays_within_tolerance(cuda_device):
-    """A wide block table (>32 columns) groups blocks per split; the same sequences then
-    merge fewer partials.  Both layouts agree with the oracle and with each other."""
+def test_decode_table_width_stays_within_tolerance(cuda_device):
+    """The block-table width sizes the work split (and the workspace); a wider table
+    changes how many partial states the same sequences produce.  Both agree with the
+    oracle."""
     q, kc, vc, bt, ctx = _case(16, B=8, hq=32, hkv=8, bs=256, lo=2000, hi=8192, width=40)
     d = cuda_device
     wide = _decode(q.to(d), kc.to(d), vc.to(d), ctx.to(d), bt.to(d)).cpu().float()
