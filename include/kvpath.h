@@ -97,7 +97,8 @@ size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q_heads, int
  * outside [0, num_cache_blocks) or a context longer than
  * max_blocks_per_seq * block_size makes that sequence's output NaN instead of
  * reading out of bounds.  block_size must be a multiple of 64.
- * The output row of head h is out + b*out_seq_stride + h*out_head_stride.
+ * The output row of head h is out + b*out_seq_stride + h*out_head_stride (out
+ * 16-byte aligned, both strides multiples of 8 elements).
  */
 int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
                           const void* k_cache, const void* v_cache,

@@ -43,9 +43,8 @@ namespace kvp {
 constexpr int kDecodeHeadDim = 128;
 constexpr int kDecodeWaves = 4;  // kv heads per workgroup
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
-constexpr int kStepTokens = 16;
-constexpr int kStepLoads = kStepTokens / 4;  // dwordx4 loads per lane per tensor per step
-constexpr int kMinStepsPerRange = 16;        // a range covers at least 256 tokens
+constexpr int kMinRangeTokens = 512;        // a range covers at least 512 tokens
+constexpr int kMinStepTokens = 16;           // smallest step (G = 8); G <= 4 steps 32 tokens
 constexpr int kMaxSeqsPerLaunch = 4096;      // size of the LDS prefix-sum table
 constexpr int kHeaderInts = 16;              // workspace header before the prefix table
 
@@ -65,6 +64,7 @@ struct DecodeParams {
   int32_t block_size;
   int32_t max_blocks;
   int32_t max_parts;  // partial states per (sequence, query head) the workspace holds
+  int32_t step_tokens;  // tokens per step (the kernel's STEP)
   float scale_log2;   // softmax_scale * log2(e)
   uint16_t* out;
   int64_t o_seq_stride, o_head_stride;
@@ -80,7 +80,7 @@ __device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
 // Steps of a sequence; 0 for empty or impossible contexts (written separately).
 __device__ __forceinline__ int seq_steps(int ctx, const DecodeParams& p) {
   if (ctx <= 0 || ctx > p.max_blocks * p.block_size) return 0;
-  return (ctx + kStepTokens - 1) / kStepTokens;
+  return (ctx + p.step_tokens - 1) / p.step_tokens;
 }
 
 // s_cum[b] = steps of sequences 0..b-1 (b = 0..num_seqs), built by the whole workgroup:
@@ -97,6 +97,20 @@ __device__ void build_step_prefix(const DecodeParams& p, int* s_cum, int* s_part
     if (b < B) local += seq_steps(p.context_lens[b], p);
   }
   s_part[tid] = local;
+  // Rows with nothing to attend (ctx 0: graph padding) read as zeros; impossible
+  // lengths read as NaN.  Neither has steps.  Workgroup w writes rows b == w (mod grid).
+  for (int i = 0; i < per; ++i) {
+    const int b = j0 + i;
+    if (b >= B || b % static_cast<int>(gridDim.x) != static_cast<int>(blockIdx.x)) continue;
+    const int ctx = p.context_lens[b];
+    if (ctx > 0 && ctx <= p.max_blocks * p.block_size) continue;
+    const uint16_t fill = ctx <= 0 ? 0 : 0x7fc0;
+    for (int o = 0; o < p.num_q_heads * kDecodeHeadDim; o += 8) {
+      const int h = o / kDecodeHeadDim, d = o - h * kDecodeHeadDim;
+      const uint4 f = make_uint4(fill * 0x10001u, fill * 0x10001u, fill * 0x10001u, fill * 0x10001u);
+      *reinterpret_cast<uint4*>(p.out + b * p.o_seq_stride + h * p.o_head_stride + d) = f;
+    }
+  }
   __syncthreads();
   for (int off = 1; off < kDecodeThreads; off <<= 1) {
     const int v = tid >= off ? s_part[tid - off] : 0;
@@ -148,9 +162,10 @@ __device__ __forceinline__ void cursor_start_seq(const DecodeParams& p, StepCurs
 // of valid tokens of the step.  On entering a block it takes the id prefetched one
 // block earlier (or loads it) and prefetches the next block's id, so the scalar load
 // is off the critical path.
+template <int STEP>
 __device__ __forceinline__ int64_t step_base(const DecodeParams& p, StepCursor& cur, int64_t head_off,
                                             int& nvalid) {
-  const int t0 = cur.j * kStepTokens;
+  const int t0 = cur.j * STEP;
   const int lblk = t0 / p.block_size;
   if (lblk != cur.lblk) {
     const int32_t* row = p.block_tables + cur.b * p.bt_stride;
@@ -163,34 +178,35 @@ __device__ __forceinline__ int64_t step_base(const DecodeParams& p, StepCursor& 
     cur.lblk = lblk;
     cur.pf_blk = (lblk + 1) * p.block_size < cur.ctx ? row[lblk + 1] : -1;
   }
-  nvalid = min(kStepTokens, cur.ctx - t0);
+  nvalid = min(STEP, cur.ctx - t0);
   return static_cast<int64_t>(cur.blk) * p.blk_stride +
          static_cast<int64_t>(t0 - lblk * p.block_size) * p.slot_stride + head_off;
 }
 
 // Token 4i + r of the step, clamped onto the last valid token so every load is in
 // bounds and needs no branch; clamped tokens are masked out of the softmax.
+template <int NL>
 __device__ __forceinline__ void step_load(const DecodeParams& p, int64_t base, int nvalid, int r,
-                                          uint4 (&kr)[kStepLoads], uint4 (&vr)[kStepLoads]) {
+                                          uint4 (&kr)[NL], uint4 (&vr)[NL]) {
 #pragma unroll
-  for (int i = 0; i < kStepLoads; ++i) {
+  for (int i = 0; i < NL; ++i) {
     const int t = min(4 * i + r, nvalid - 1);
     kr[i] = load16(p.k_cache + base + t * p.slot_stride);
     vr[i] = load16(p.v_cache + base + t * p.slot_stride);
   }
 }
 
-template <int G>
+template <int G, int NL>
 __device__ __forceinline__ void step_compute(const DecodeParams& p, const uint4 (&qv)[G],
-                                             const uint4 (&kr)[kStepLoads], const uint4 (&vr)[kStepLoads],
+                                             const uint4 (&kr)[NL], const uint4 (&vr)[NL],
                                              int nvalid, int r, float (&m)[G], float (&l)[G],
                                              float (&acc)[G][8]) {
-  float s[G][kStepLoads];
+  float s[G][NL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float mx = kMaxFloor;
 #pragma unroll
-    for (int i = 0; i < kStepLoads; ++i) {
+    for (int i = 0; i < NL; ++i) {
       float part = dot2_bf16(qv[g].x, kr[i].x, 0.f);
       part = dot2_bf16(qv[g].y, kr[i].y, part);
       part = dot2_bf16(qv[g].z, kr[i].z, part);
@@ -208,7 +224,7 @@ __device__ __forceinline__ void step_compute(const DecodeParams& p, const uint4 
   }
   // P V: each V row is widened to fp32 once and feeds all G heads.
 #pragma unroll
-  for (int i = 0; i < kStepLoads; ++i) {
+  for (int i = 0; i < NL; ++i) {
     const float vf[8] = {bf16_lo(vr[i].x), bf16_hi(vr[i].x), bf16_lo(vr[i].y), bf16_hi(vr[i].y),
                          bf16_lo(vr[i].z), bf16_hi(vr[i].z), bf16_lo(vr[i].w), bf16_hi(vr[i].w)};
 #pragma unroll
@@ -265,9 +281,11 @@ __device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh
   }
 }
 
-template <int G>
+template <int G, int STEP>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const DecodeParams p) {
   constexpr int D = kDecodeHeadDim;
+  constexpr int NL = STEP / 4;  // dwordx4 loads per lane per tensor per step
+  constexpr int kMinSteps = kMinRangeTokens / STEP;
   __shared__ int s_cum[kMaxSeqsPerLaunch + 1];
   __shared__ int s_part[kDecodeThreads];
 
@@ -277,24 +295,12 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   const int r = lane >> 4;
   const int c = lane & 15;
 
-  // Rows with nothing to attend (ctx 0: graph padding) read as zeros; impossible
-  // lengths read as NaN.  Neither has steps.
-  for (int b = blockIdx.x; b < p.num_seqs; b += gridDim.x) {
-    const int ctx = p.context_lens[b];
-    if (ctx > 0 && ctx <= p.max_blocks * p.block_size) continue;
-    const uint16_t fill = ctx <= 0 ? 0 : 0x7fc0;
-    for (int o = tid; o < p.num_q_heads * D; o += kDecodeThreads) {
-      const int h = o / D, d = o - h * D;
-      p.out[b * p.o_seq_stride + h * p.o_head_stride + d] = fill;
-    }
-  }
-
   build_step_prefix(p, s_cum, s_part);
   const int B = p.num_seqs;
   const int total_steps = s_cum[B];
   const int groups_per_range = (p.num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
   const int num_ranges = max(1, static_cast<int>(gridDim.x) / groups_per_range);
-  const int spr = max(kMinStepsPerRange, (total_steps + num_ranges - 1) / num_ranges);
+  const int spr = max(kMinSteps, (total_steps + num_ranges - 1) / num_ranges);
   if (blockIdx.x == 0) {  // for the merge kernel
     if (tid == 0) p.header[0] = spr;
     for (int b = tid; b <= B; b += kDecodeThreads) p.header[kHeaderInts + b] = s_cum[b];
@@ -330,14 +336,14 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
   }
 
-  uint4 kA[kStepLoads], vA[kStepLoads], kB[kStepLoads], vB[kStepLoads];
+  uint4 kA[NL], vA[NL], kB[NL], vB[NL];
   int nvA, nvB = 0;
-  step_load(p, step_base(p, cur, head_off, nvA), nvA, r, kA, vA);
+  step_load<NL>(p, step_base<STEP>(p, cur, head_off, nvA), nvA, r, kA, vA);
 
   // One step: prefetch the next step into (kN, vN), compute (kC, vC), emit at the end
   // of a sequence or of the range.  Returns false when the range is done.
-  auto advance = [&](uint4 (&kC)[kStepLoads], uint4 (&vC)[kStepLoads], int nvC,
-                     uint4 (&kN)[kStepLoads], uint4 (&vN)[kStepLoads], int& nvN, int S) -> bool {
+  auto advance = [&](uint4 (&kC)[NL], uint4 (&vC)[NL], int nvC,
+                     uint4 (&kN)[NL], uint4 (&vN)[NL], int& nvN, int S) -> bool {
     const bool more = S + 1 < S1;
     const bool seq_end = cur.j + 1 == cur.nsteps;
     StepCursor nxt = cur;
@@ -354,9 +360,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       } else {
         nxt.j = cur.j + 1;
       }
-      step_load(p, step_base(p, nxt, head_off, nvN), nvN, r, kN, vN);
+      step_load<NL>(p, step_base<STEP>(p, nxt, head_off, nvN), nvN, r, kN, vN);
     }
-    step_compute<G>(p, qv, kC, vC, nvC, r, m, l, acc);
+    step_compute<G, NL>(p, qv, kC, vC, nvC, r, m, l, acc);
     if (seq_end || !more) {
       const int cb = s_cum[cur.b], cb1 = s_cum[cur.b + 1];
       const int np = num_parts(cb, cb1, spr);
@@ -384,21 +390,26 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 }
 
 // Combines the per-range partial states of sequences that span several ranges.
-// grid = (num_q_heads, num_seqs), 128 threads (one per head dim).
-__global__ __launch_bounds__(kDecodeHeadDim) void decode_merge_kernel(const DecodeParams p) {
+// grid = (ceil(num_q_heads / 8), num_seqs), 1024 threads: 8 query heads x 128 dims,
+// one output element per thread (few, large workgroups: dispatch is the main cost).
+constexpr int kMergeHeads = 8;
+__global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_kernel(const DecodeParams p) {
   constexpr int D = kDecodeHeadDim;
-  const int h = blockIdx.x;
+  const int h = blockIdx.x * kMergeHeads + static_cast<int>(threadIdx.x) / D;
   const int b = blockIdx.y;
-  const int d = threadIdx.x;
+  const int d = threadIdx.x % D;
+  if (h >= p.num_q_heads) return;
   const int cb = p.header[kHeaderInts + b], cb1 = p.header[kHeaderInts + b + 1];
   if (cb1 <= cb) return;  // no steps: written by the main kernel
   const int np = num_parts(cb, cb1, p.header[0]);
-  if (np <= 1) return;
+  if (np <= 1) return;  // written by the main kernel
   const int64_t row0 = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.max_parts;
   const float* ml = p.part_ml + row0 * 2;
   float mm = kMaxFloor;
+#pragma unroll 4
   for (int s = 0; s < np; ++s) mm = fmaxf(mm, ml[2 * s]);
   float ll = 0.f, oo = 0.f;
+#pragma unroll 4
   for (int s = 0; s < np; ++s) {
     const float w = fast_exp2(ml[2 * s] - mm);
     ll += w * ml[2 * s + 1];
@@ -407,11 +418,12 @@ __global__ __launch_bounds__(kDecodeHeadDim) void decode_merge_kernel(const Deco
   p.out[b * p.o_seq_stride + h * p.o_head_stride + d] = f32_to_bf16(oo / ll);
 }
 
-// Partial states per (sequence, query head): a sequence of at most max_tokens tokens
-// spans at most ceil(steps / kMinStepsPerRange) + 1 ranges.
+// Partial states per (sequence, query head): ranges hold at least kMinRangeTokens
+// tokens (whole steps of at least kMinStepTokens), so a sequence of up to max_tokens
+// tokens meets at most ceil(max_tokens / kMinRangeTokens) + 1 of them.
 static int64_t decode_max_parts(int64_t max_blocks, int64_t block_size) {
-  const int64_t steps = (max_blocks * block_size + kStepTokens - 1) / kStepTokens;
-  return (steps + kMinStepsPerRange - 1) / kMinStepsPerRange + 1;
+  const int64_t tokens = max_blocks * block_size;
+  return (tokens + kMinRangeTokens - 1) / kMinRangeTokens + 1;
 }
 
 static int64_t decode_workspace_need(int64_t seqs, int64_t q_heads, int64_t max_parts) {
@@ -421,7 +433,7 @@ static int64_t decode_workspace_need(int64_t seqs, int64_t q_heads, int64_t max_
 }
 
 // Workgroups of paged_decode_kernel<G> resident on the whole current device.
-template <int G>
+template <int G, int STEP>
 static int resident_workgroups() {
   static std::atomic<int> cached[16];
   int dev = 0;
@@ -431,7 +443,7 @@ static int resident_workgroups() {
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<G>, kDecodeThreads, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<G, STEP>, kDecodeThreads, 0) !=
           hipSuccess || per_cu <= 0)
     per_cu = 1;
   v = cus * per_cu;
@@ -439,19 +451,22 @@ static int resident_workgroups() {
   return v;
 }
 
-template <int G>
-static void launch_decode(const DecodeParams& p, int64_t max_steps, hipStream_t s) {
+template <int G, int STEP>
+static void launch_decode(DecodeParams p, int64_t max_tokens, hipStream_t s) {
   static const int forced = [] {
     const char* env = getenv("KVP_DECODE_GRID");
     return env ? atoi(env) : 0;
   }();
   const int64_t groups_per_range = (p.num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
-  const int64_t grid0 = forced > 0 ? forced : resident_workgroups<G>();
+  const int64_t grid0 = forced > 0 ? forced : resident_workgroups<G, STEP>();
   // no more ranges than minimum-size ranges over the largest possible work
-  const int64_t max_ranges = std::max<int64_t>(1, (max_steps + kMinStepsPerRange - 1) / kMinStepsPerRange);
+  const int64_t max_ranges = std::max<int64_t>(1, (max_tokens + kMinRangeTokens - 1) / kMinRangeTokens);
+  p.step_tokens = STEP;
   const int64_t ranges = std::max<int64_t>(1, std::min<int64_t>(grid0 / groups_per_range, max_ranges));
   const int64_t grid = ranges * groups_per_range;
-  hipLaunchKernelGGL(paged_decode_kernel<G>, dim3(static_cast<unsigned>(grid)), dim3(kDecodeThreads), 0, s, p);
+  hipLaunchKernelGGL((paged_decode_kernel<G, STEP>), dim3(static_cast<unsigned>(grid)), dim3(kDecodeThreads), 0, s, p);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((p.num_q_heads + kMergeHeads - 1) / kMergeHeads, p.num_seqs),
+                     dim3(kMergeHeads * kDecodeHeadDim), 0, s, p);
 }
 
 }  // namespace kvp
@@ -505,12 +520,13 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
     return fail(KVP_EINVAL, "kvp_paged_decode_bf16: null pointer");
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
     return fail(KVP_EINVAL, "kvp_paged_decode_bf16: q and cache pointers must be 16-byte aligned");
-  if ((reinterpret_cast<uintptr_t>(out) & 1u) || (reinterpret_cast<uintptr_t>(block_tables) & 3u) ||
+  if (!aligned16(out) || (reinterpret_cast<uintptr_t>(block_tables) & 3u) ||
       (reinterpret_cast<uintptr_t>(context_lens) & 3u))
     return fail(KVP_EINVAL, "kvp_paged_decode_bf16: misaligned out/block_tables/context_lens");
   if (!mult8(q_seq_stride) || !mult8(q_head_stride) || !mult8(cache_block_stride) ||
-      !mult8(cache_slot_stride) || !mult8(cache_head_stride))
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: q and cache strides must be multiples of 8 elements");
+      !mult8(cache_slot_stride) || !mult8(cache_head_stride) || !mult8(out_seq_stride) ||
+      !mult8(out_head_stride))
+    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: q, cache and out strides must be multiples of 8 elements");
 
   const int chunk_seqs = std::min(num_seqs, kMaxSeqsPerLaunch);
   const int64_t max_parts = decode_max_parts(max_blocks_per_seq, block_size);
@@ -523,7 +539,6 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t header_bytes = (((kHeaderInts + kMaxSeqsPerLaunch + 1) * 4) + 255) / 256 * 256;
-  const int64_t steps_per_seq = (static_cast<int64_t>(max_blocks_per_seq) * block_size + kStepTokens - 1) / kStepTokens;
   // Batches beyond the LDS prefix table run as consecutive launches of up to 4096
   // sequences; they reuse the workspace in stream order.
   for (int b0 = 0; b0 < num_seqs; b0 += kMaxSeqsPerLaunch) {
@@ -556,17 +571,14 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
     p.part_o = reinterpret_cast<float*>(ws + header_bytes);
     p.part_ml = p.part_o + static_cast<size_t>(nb) * num_q_heads * max_parts * kDecodeHeadDim;
 
-    const int64_t max_steps = static_cast<int64_t>(nb) * steps_per_seq;
+    const int64_t max_tokens = static_cast<int64_t>(nb) * max_blocks_per_seq * block_size;
     switch (G) {
-      case 1: launch_decode<1>(p, max_steps, s); break;
-      case 2: launch_decode<2>(p, max_steps, s); break;
-      case 4: launch_decode<4>(p, max_steps, s); break;
-      default: launch_decode<8>(p, max_steps, s); break;
+      case 1: launch_decode<1, 32>(p, max_tokens, s); break;
+      case 2: launch_decode<2, 32>(p, max_tokens, s); break;
+      case 4: launch_decode<4, 32>(p, max_tokens, s); break;
+      default: launch_decode<8, kMinStepTokens>(p, max_tokens, s); break;
     }
-    int rc = launch_status("kvp_paged_decode_bf16");
-    if (rc != KVP_OK) return rc;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(num_q_heads, nb), dim3(kDecodeHeadDim), 0, s, p);
-    rc = launch_status("kvp_paged_decode_bf16 (merge)");
+    const int rc = launch_status("kvp_paged_decode_bf16");
     if (rc != KVP_OK) return rc;
   }
   return KVP_OK;
