@@ -36,11 +36,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(x >> 16);
 }
 
-__device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
-  return static_cast<u32>(f32_to_bf16(lo)) | (static_cast<u32>(f32_to_bf16(hi)) << 16);
-}
-
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(u32, v);
+}
 
 // a.lo*b.lo + a.hi*b.hi + acc on packed bf16 pairs, accumulated in fp32 (v_dot2c_f32_bf16).
 __device__ __forceinline__ float dot2_bf16(u32 a, u32 b, float acc) {

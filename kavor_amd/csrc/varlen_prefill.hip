@@ -11,9 +11,11 @@
 //   A workgroup (4 waves) owns one (sequence, kv head, query tile) and all G query heads
 //   of that kv head: 128 "rows" = 128/G query tokens x G heads, row rho = tok*G + g, so a
 //   staged K/V tile feeds G heads.  Wave w owns rows [32w, 32w+32).
-//   Per 64-key tile the workgroup stages K row-major and V transposed in LDS, then each
-//   wave computes S^T = K Q^T (M = 64 keys, N = 32 rows, K-dim = 128) and
-//   O^T += V^T P^T (M = 128 dims, N = 32 rows, K-dim = 64 keys).  With the transposed
+//   Per 64-key tile the workgroup stages K and V row-major in LDS (double-buffered, one
+//   barrier per tile; the next tile's global loads are in flight during the MFMAs),
+//   then each wave computes S^T = K Q^T (M = 64 keys, N = 32 rows, K-dim = 128) and
+//   O^T += V^T P^T (M = 128 dims, N = 32 rows, K-dim = 64 keys), reading the V^T operand
+//   with the gfx950 LDS transpose load (ds_read_b64_tr_b16).  With the transposed
 //   products every lane holds whole columns of its own query row (row = lane % 32), so
 //   the online-softmax max / sum / rescale need only one cross-lane exchange (lane^32)
 //   and P feeds the second MFMA straight from registers.
@@ -33,7 +35,7 @@ constexpr int kPrefillWaves = 4;
 constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows (token x head) per workgroup
 constexpr int kKeyTile = 64;
 constexpr int kKStride = kPrefillHeadDim + 8;  // LDS row pitch of the K tile (bf16)
-constexpr int kVtStride = kKeyTile + 8;        // LDS row pitch of the transposed V tile (bf16)
+constexpr int kVStride = kPrefillHeadDim + 8;  // LDS row pitch of the V tile (bf16)
 constexpr int kNumXcd = 8;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -60,6 +62,16 @@ struct PrefillParams {
   uint16_t* out;
   int64_t o_tok_stride, o_head_stride;
 };
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: 8 bytes per lane, transposed as 16-bit elements across each
+// 16-lane group (see the V^T operand in the kernel).
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* lds_ptr) {
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t*)(lds_ptr));
+  return __builtin_bit_cast(uint2, v);
+}
 
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -94,12 +106,53 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
   bool bad = false;
   if (PAGED && klen > p.max_blocks * p.block_size) bad = true;
 
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[kKeyTile * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * kVtStride];
+  // Two buffers of the K and V tiles (row-major, padded rows): tile i+1 is written while
+  // other waves may still read tile i.
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKeyTile * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kKeyTile * kVStride];
   __shared__ int s_bad;
 
   if (tid == 0) s_bad = 0;  // sticky for the workgroup: one sequence, one block table
   __syncthreads();
+
+  // Thread t stages 16-byte chunk (t % 16) of keys t/16 + 16u, u = 0..3, of a 64-key tile.
+  const int chunk = tid & 15;
+  auto load_tile = [&](int kv0, uint4 (&kc)[4], uint4 (&vc)[4]) {
+    int64_t kbase = 0, vbase = 0;
+    bool blk_ok = true;
+    if (PAGED) {
+      const int lblk = kv0 / p.block_size;
+      int blk = (lblk < p.max_blocks) ? p.block_tables[s * p.bt_stride + lblk] : -1;
+      if (blk < 0 || blk >= p.num_cache_blocks) {
+        blk_ok = false;
+        blk = 0;
+      }
+      const int off = kv0 - lblk * p.block_size;
+      kbase = static_cast<int64_t>(blk) * p.k_blk_stride + static_cast<int64_t>(off) * p.k_tok_stride;
+      vbase = static_cast<int64_t>(blk) * p.v_blk_stride + static_cast<int64_t>(off) * p.v_tok_stride;
+    } else {
+      kbase = static_cast<int64_t>(k_start + kv0) * p.k_tok_stride;
+      vbase = static_cast<int64_t>(k_start + kv0) * p.v_tok_stride;
+    }
+    if (!blk_ok) bad = true;
+    kbase += static_cast<int64_t>(kvh) * p.k_head_stride + 8 * chunk;
+    vbase += static_cast<int64_t>(kvh) * p.v_head_stride + 8 * chunk;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int key = (tid >> 4) + 16 * u;
+      const bool ok = kv0 + key < klen && blk_ok;
+      kc[u] = ok ? *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride) : make_uint4(0, 0, 0, 0);
+      vc[u] = ok ? *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride) : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  // V^T operand of O^T = V^T P^T via the LDS transpose read: within each 16-lane group
+  // ds_read_b64_tr_b16 hands lane i element e = element (i % 4) of the 8 bytes addressed
+  // by lane 4e + i/4.  Lane L therefore addresses key 4*hf + (L%16)/4 (+16kk, +8 for the
+  // upper half) at dims 32mb + 16*((L/16)%2) + 4*(L%4): it receives dim 32mb + L%32 of
+  // keys 4hf + e, which is the key order of this lane's P registers.
+  const int tr_key = 4 * hf + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   const int ntiles_seq = (qlen + TOK - 1) / TOK;
   // Grid-stride over query tiles (a sequence longer than the grid's max_seqlen_q is
@@ -126,6 +179,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
 
     const int q_last = min(qlen, q0 + TOK) - 1;
     const int kv_end = CAUSAL ? min(klen, q_last + diag + 1) : klen;
+    const int nkv = kv_end > 0 ? (kv_end + kKeyTile - 1) / kKeyTile : 0;
 
     f32x16_t oacc[D / 32];
 #pragma unroll
@@ -134,52 +188,23 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
       for (int j = 0; j < 16; ++j) oacc[mb][j] = 0.f;
     float m_run = kMaxFloor, l_run = 0.f;
     const int row_limit = CAUSAL ? qi + diag : klen - 1;  // last key this row may see
+    // smallest row_limit over this wave's rows (its first query token)
+    const int wave_min_limit = CAUSAL ? q0 + (32 * wave) / G + diag : klen - 1;
 
-    for (int kv0 = 0; kv0 < kv_end; kv0 += kKeyTile) {
-      __syncthreads();  // previous tile fully consumed
-      // ---- stage K (row-major) and V (transposed) for keys [kv0, kv0 + 64)
-      {
-        const int chunk = tid & 15;
-        int64_t kbase = 0, vbase = 0;
-        bool blk_ok = true;
-        if (PAGED) {
-          const int lblk = kv0 / p.block_size;
-          int blk = (lblk < p.max_blocks) ? p.block_tables[s * p.bt_stride + lblk] : -1;
-          if (blk < 0 || blk >= p.num_cache_blocks) {
-            blk_ok = false;
-            blk = 0;
-          }
-          const int off = kv0 - lblk * p.block_size;
-          kbase = static_cast<int64_t>(blk) * p.k_blk_stride + static_cast<int64_t>(off) * p.k_tok_stride;
-          vbase = static_cast<int64_t>(blk) * p.v_blk_stride + static_cast<int64_t>(off) * p.v_tok_stride;
-        } else {
-          kbase = static_cast<int64_t>(k_start + kv0) * p.k_tok_stride;
-          vbase = static_cast<int64_t>(k_start + kv0) * p.v_tok_stride;
-        }
-        if (!blk_ok) bad = true;
-        kbase += static_cast<int64_t>(kvh) * p.k_head_stride + 8 * chunk;
-        vbase += static_cast<int64_t>(kvh) * p.v_head_stride + 8 * chunk;
-        uint4 kc[4], vc[4];
+    uint4 kc[4], vc[4];
+    if (nkv > 0) load_tile(0, kc, vc);
+    for (int it = 0; it < nkv; ++it) {
+      const int kv0 = it * kKeyTile;
+      uint16_t* sk = s_k[it & 1];
+      uint16_t* sv = s_v[it & 1];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int key = (tid >> 4) + 16 * u;
-          const bool ok = kv0 + key < klen && blk_ok;
-          kc[u] = ok ? *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride) : make_uint4(0, 0, 0, 0);
-          vc[u] = ok ? *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int key = (tid >> 4) + 16 * u;
-          *reinterpret_cast<uint4*>(&s_k[key * kKStride + 8 * chunk]) = kc[u];
-          const u32 w[4] = {vc[u].x, vc[u].y, vc[u].z, vc[u].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            s_vt[(8 * chunk + 2 * e) * kVtStride + key] = static_cast<uint16_t>(w[e] & 0xffffu);
-            s_vt[(8 * chunk + 2 * e + 1) * kVtStride + key] = static_cast<uint16_t>(w[e] >> 16);
-          }
-        }
+      for (int u = 0; u < 4; ++u) {
+        const int key = (tid >> 4) + 16 * u;
+        *reinterpret_cast<uint4*>(&sk[key * kKStride + 8 * chunk]) = kc[u];
+        *reinterpret_cast<uint4*>(&sv[key * kVStride + 8 * chunk]) = vc[u];
       }
-      __syncthreads();
+      __syncthreads();  // tile `it` staged; every wave is done with tile it-1's buffer
+      if (it + 1 < nkv) load_tile(kv0 + kKeyTile, kc, vc);  // in flight during the MFMAs
 
       // ---- S^T = K Q^T : two 32-key blocks, lane holds keys of its own query row
       f32x16_t sacc[2];
@@ -189,48 +214,64 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
         for (int j = 0; j < 16; ++j) sacc[mb][j] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) {
-          const uint4 a = *reinterpret_cast<const uint4*>(&s_k[(32 * mb + n) * kKStride + 16 * ks + 8 * hf]);
+          const uint4 a = *reinterpret_cast<const uint4*>(&sk[(32 * mb + n) * kKStride + 16 * ks + 8 * hf]);
           sacc[mb] = mfma32(a, qreg[ks], sacc[mb]);
         }
       }
 
-      // ---- online softmax over this tile (base 2)
+      // ---- online softmax over this tile (base 2).  Interior tiles (every key visible
+      // to every row of the wave) skip the mask.  The running max only moves when a row's
+      // tile max exceeds it by more than 2^8, so O is rescaled rarely; P <= 2^8 stays
+      // exact enough in bf16 (the relative precision does not depend on magnitude).
+      const bool interior = kv0 + kKeyTile - 1 <= min(klen - 1, wave_min_limit);
       float mx = kMaxFloor;
+      if (interior) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = kv0 + 32 * mb + 8 * (j >> 2) + 4 * hf + (j & 3);
-          const bool ok = key < klen && key <= row_limit;
-          const float x = ok ? sacc[mb][j] * p.scale_log2 : -INFINITY;
-          sacc[mb][j] = x;
-          mx = fmaxf(mx, x);
-        }
+          for (int j = 0; j < 16; ++j) {
+            sacc[mb][j] *= p.scale_log2;
+            mx = fmaxf(mx, sacc[mb][j]);
+          }
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = kv0 + 32 * mb + 8 * (j >> 2) + 4 * hf + (j & 3);
+            const bool ok = key < klen && key <= row_limit;
+            sacc[mb][j] = ok ? sacc[mb][j] * p.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, sacc[mb][j]);
+          }
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
+      const bool grow = mx > m_run + 8.f;
+      if (__any(grow)) {
+        const float m_new = grow ? mx : m_run;
+        const float alpha = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int mb = 0; mb < D / 32; ++mb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) oacc[mb][j] *= alpha;
+      }
       float rsum = 0.f;
       u32 pk[2][8];  // P as packed bf16 pairs: [mb][pair]
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
-          const float p0 = fast_exp2(sacc[mb][j] - m_new);
-          const float p1 = fast_exp2(sacc[mb][j + 1] - m_new);
+          const float p0 = fast_exp2(sacc[mb][j] - m_run);
+          const float p1 = fast_exp2(sacc[mb][j + 1] - m_run);
           rsum += p0 + p1;
           pk[mb][j >> 1] = pack_bf16x2(p0, p1);
         }
       rsum += __shfl_xor(rsum, 32);
-      l_run = l_run * alpha + rsum;
-#pragma unroll
-      for (int mb = 0; mb < D / 32; ++mb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) oacc[mb][j] *= alpha;
+      l_run += rsum;
 
       // ---- O^T += V^T P^T : K-dim step kk covers keys 16kk..16kk+15.  This lane's P
-      // registers for that step hold key offsets {4hf+0..3, 8+4hf+0..3}; the V^T operand
-      // is read with the same key order.
+      // registers for that step hold key offsets {4hf+0..3, 8+4hf+0..3}.
 #pragma unroll
       for (int kk = 0; kk < kKeyTile / 16; ++kk) {
         const int mbs = kk >> 1;
@@ -238,9 +279,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
         const uint4 b = make_uint4(pk[mbs][pj], pk[mbs][pj + 1], pk[mbs][pj + 2], pk[mbs][pj + 3]);
 #pragma unroll
         for (int mb = 0; mb < D / 32; ++mb) {
-          const uint16_t* vrow = &s_vt[(32 * mb + n) * kVtStride + 16 * kk + 4 * hf];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+          const uint16_t* vp = &sv[(16 * kk + tr_key) * kVStride + 32 * mb + tr_dim];
+          const uint2 lo = lds_read_tr16(vp);
+          const uint2 hi = lds_read_tr16(vp + 8 * kVStride);
           oacc[mb] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), b, oacc[mb]);
         }
       }
