@@ -121,7 +121,7 @@ def bench_append(dev, steps, warmup):
         it[0] += 1
         store_kvcache(k, v, kc, vc, s)
 
-    ms = time_launches(step, max(steps, 48), warmup)
+    ms = time_launches(step, steps if steps < 16 else max(steps, 48), warmup)
     nbytes = append_bytes(sets[0][2].cpu().numpy(), hkv, D)
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
 
@@ -206,6 +206,129 @@ def load_traffic(name: str):
         return None
 
 
+def profile_run(dev) -> int:
+    """Fixed launch sequence for rocprofv3 counter runs: 3 plain 1 GiB copies (the
+    calibration of the byte counters), then (after warm-up launches) 10 decode steps of
+    the Qwen3-0.6B workload, 10 KV appends, 3 prefix-cached prefills and 3 decode steps
+    of the Qwen3-8B workload."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    bench_decode(dev, 10, 3, "qwen3_0.6b")
+    torch.cuda.empty_cache()
+    bench_append(dev, 10, 3)
+    torch.cuda.empty_cache()
+    bench_prefill(dev, 3, 1)
+    torch.cuda.empty_cache()
+    bench_decode(dev, 3, 1, "qwen3_8b")
+    torch.cuda.synchronize()
+    print("profile run done", flush=True)
+    return 0
+
+
+PROFILE_CMDS = [
+    "cd /tmp && export TMPDIR=/tmp",
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/pmc_trace -o run -- python $R/bench.py --profile",
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_fetch -o run -- python $R/bench.py --profile",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_write -o run -- python $R/bench.py --profile",
+    "python $R/bench.py --summarize $R/gpurun_out/pmc_trace $R/gpurun_out/pmc_fetch $R/gpurun_out/pmc_write",
+]
+
+# (profile file, kernel-name prefix, which occurrence group, algorithmic bytes or flops, unit)
+PROFILE_KERNELS = [
+    ("paged_decode_qwen3_0.6b", "void kvp::paged_decode_kernel<2,", "decode_0.6b"),
+    ("paged_decode_qwen3_8b", "void kvp::paged_decode_kernel<4,", "decode_8b"),
+    ("kv_append_4096tok", "void kvp::kv_append_kernel<128>", "append"),
+    ("varlen_prefill_prefix_32seq", "void kvp::varlen_prefill_kernel<2, true, true>", "prefill"),
+]
+
+
+def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
+    """Per-kernel duration and HBM traffic from the three rocprofv3 runs of --profile.
+
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are scaled by what they read for the plain
+    1 GiB device copies that start the run (largest __amd_rocclr_copyBuffer dispatches)."""
+    import csv
+    from collections import defaultdict
+
+    def rows(d, name):
+        with open(Path(d) / name) as f:
+            return list(csv.DictReader(f))
+
+    trace = rows(trace_dir, "run_kernel_trace.csv")
+    dur = defaultdict(list)
+    for r in trace:
+        dur[r["Kernel_Name"]].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    counters = {}
+    for d, cname in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+        vals = defaultdict(list)
+        for r in rows(d, "run_counter_collection.csv"):
+            if r["Counter_Name"] == cname:
+                vals[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        counters[cname] = vals
+    gib_kib = float(1 << 20)
+    copy_f = max(counters["FETCH_SIZE"]["__amd_rocclr_copyBuffer"])
+    copy_w = max(counters["WRITE_SIZE"]["__amd_rocclr_copyBuffer"])
+    f_scale, w_scale = gib_kib / copy_f, gib_kib / copy_w
+    algo = {  # algorithmic bytes (flops for prefill) per launch of each workload
+        "decode_0.6b": _decode_algo_bytes(256, 16, 100, 2048, 4096),
+        "decode_8b": _decode_algo_bytes(128, 32, 1024, 32768, 20000),
+        "append": 32522240,
+        "prefill": 352688504832,
+    }
+    out_dir = ROOT / "profiles"
+    out_dir.mkdir(exist_ok=True)
+    merge_name = "kvp::decode_merge_kernel(kvp::DecodeParams)"
+    for fname, prefix, key in PROFILE_KERNELS:
+        names = [n for n in dur if n.startswith(prefix)]
+        if not names:
+            continue
+        name = names[0]
+        d_us = [x / 1e3 for x in dur[name]]
+        fetch = [x * f_scale * 1024 for x in counters["FETCH_SIZE"].get(name, [])]
+        write = [x * w_scale * 1024 for x in counters["WRITE_SIZE"].get(name, [])]
+        avg_us = statistics.mean(d_us)
+        traffic = (statistics.mean(fetch) if fetch else 0) + (statistics.mean(write) if write else 0)
+        lines = [f"# {fname}: `{name}`", "",
+                 "Commands (from the repository root on the GPU host, `R=$PWD`):", "", "```"]
+        lines += PROFILE_CMDS + ["```", ""]
+        lines += [f"- dispatches: {len(d_us)}; duration avg {avg_us:.2f} us, min {min(d_us):.2f}, max {max(d_us):.2f}"]
+        if key == "prefill":
+            lines += [f"- algorithmic work: {algo[key]} flop (unmasked query-key pairs x 4 x Hq x D) "
+                      f"-> {algo[key] / avg_us / 1e6:.1f} TFLOP/s at the average duration "
+                      f"({algo[key] / avg_us / 1e6 / BF16_PEAK_TFLOPS * 100:.1f}% of 2.5 PFLOP/s dense bf16)"]
+        else:
+            lines += [f"- algorithmic bytes: {algo[key]} -> {algo[key] / avg_us / 1e3:.1f} GB/s at the average "
+                      f"duration ({algo[key] / avg_us / 1e3 / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)"]
+        lines += [f"- FETCH_SIZE calibration: 1 GiB copy reads {copy_f:.1f} KiB -> scale {f_scale:.4f}; "
+                  f"WRITE_SIZE: 1 GiB copy writes {copy_w:.1f} KiB -> scale {w_scale:.4f}",
+                  f"- HBM traffic per dispatch (scaled): read {statistics.mean(fetch):.0f} B, "
+                  f"write {statistics.mean(write):.0f} B, total {traffic:.0f} B"
+                  + (f" = {traffic / algo[key]:.4f} x algorithmic" if key != "prefill" else "")]
+        if key.startswith("decode") and merge_name in dur:
+            m_us = [x / 1e3 for x in dur[merge_name]]
+            lines += [f"- the decode's split-combining `{merge_name}` (all decode workloads): "
+                      f"avg {statistics.mean(m_us):.2f} us over {len(m_us)} dispatches"]
+        (out_dir / f"{fname}.md").write_text("\n".join(lines) + "\n")
+        if key == "decode_0.6b":
+            (out_dir / "paged_decode_qwen3_0.6b_pmc.json").write_text(json.dumps(
+                {"kernel": name, "traffic_bytes": int(round(traffic)), "fetch_scale": f_scale,
+                 "write_scale": w_scale, "avg_duration_us": avg_us}, indent=1) + "\n")
+        print(f"{fname}: {avg_us:.2f} us, traffic {traffic:.0f} B", flush=True)
+    return 0
+
+
+def _decode_algo_bytes(B, hq, lo, hi, pool_blocks, seed=0):
+    from oracle.kvpath_oracle import decode_bytes
+
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(lo, hi + 1, (B,), generator=g, dtype=torch.int32)
+    return decode_bytes(ctx.tolist(), hq, 8, D, BS)
+
+
 # ----------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -215,7 +338,16 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="headline decode workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--summarize", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/*.md (and the decode traffic json) from the CSV output of "
+                         "three rocprofv3 runs of --profile: --kernel-trace --stats, --pmc "
+                         "FETCH_SIZE, --pmc WRITE_SIZE")
+    ap.add_argument("--profile", action="store_true",
+                    help="launch each kernel a few times (no timing) under rocprofv3; starts with a "
+                         "plain 1 GiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.summarize:
+        return summarize_profiles(*args.summarize)
     if args.gpus != 1:
         print(f"bench.py measures one GPU's paged KV-cache kernels; --gpus {args.gpus} is not "
               "supported (the path shards by kv head with no exchange inside attention).", file=sys.stderr)
@@ -227,6 +359,8 @@ def main() -> int:
     from kavor_amd._lib import lib
 
     lib()
+    if args.profile:
+        return profile_run(dev)
 
     inp, dec = bench_decode(dev, args.steps, args.warmup, "qwen3_0.6b")
     extras = {}
