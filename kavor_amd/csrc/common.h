@@ -71,6 +71,17 @@ __device__ __forceinline__ float row16_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef u32 u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte load / store with the nontemporal hint, for data touched exactly once (KV rows
+// streamed by attention, cache rows written by the append): it is not kept in L2.
+__device__ __forceinline__ uint4 load16_nt(const void* ptr) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr)));
+}
+__device__ __forceinline__ void store16_nt(void* ptr, uint4 v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(ptr));
+}
+
 // Lowest finite value used as the running-max floor of the online softmax, so that
 // exp2(m_old - m_new) never evaluates (-inf) - (-inf).
 constexpr float kMaxFloor = -1.0e30f;

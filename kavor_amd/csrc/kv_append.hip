@@ -8,7 +8,8 @@
 // chunks (8 bf16); the wave's lanes own consecutive chunks, so every load and store
 // is a dwordx4 and a 16-lane group covers one 256-byte head row contiguously.  Each
 // lane issues all of its loads before its first store so a wave keeps up to 4 KiB in
-// flight; the token index, slot and row addresses are wave-uniform scalars.  For Qwen3 (8 kv heads x 128) a token is 256 chunks: 4 per lane.
+// flight; the token index, slot and row addresses are wave-uniform scalars.  For Qwen3
+// (8 kv heads x 128) a token row is 128 chunks per tensor: 2 K + 2 V chunks per lane.
 #include "common.h"
 
 namespace kvp {
@@ -28,72 +29,68 @@ struct AppendParams {
   int32_t block_size;
 };
 
-constexpr int kAppendWaves = 4;     // tokens per workgroup
-constexpr int kAppendUnroll = 4;    // 16-byte chunks in flight per lane
+constexpr int kAppendWaves = 4;  // tokens per workgroup
 
-// Chunk j of a token (K chunks first, then V) -> source and destination offsets in
-// 16-byte units.  `j` is clamped by the caller so every computed address is valid.
-template <int HEAD_DIM>
-__device__ __forceinline__ void chunk_offsets(const AppendParams& p, int j, int chunks_per_tensor,
-                                              bool& is_v, int64_t& src, int64_t& dst) {
+// CPL = 16-byte chunks per lane per tensor: a token's K row and its V row are each
+// Hkv * HEAD_DIM / 8 chunks; lane l owns chunks l, l + 64, ... of both.  Every lane issues
+// all 2 * CPL loads before its first store; chunk indices are clamped onto the row's last
+// chunk, so neither loads nor stores need a branch.
+template <int HEAD_DIM, int CPL>
+__global__ __launch_bounds__(64 * kAppendWaves) void kv_append_kernel(const AppendParams p) {
   constexpr int kChunksPerHead = HEAD_DIM / 8;
-  is_v = j >= chunks_per_tensor;
-  const int jj = is_v ? j - chunks_per_tensor : j;
-  const int head = jj / kChunksPerHead;
-  const int part = jj - head * kChunksPerHead;
-  src = head * (is_v ? p.value_head_stride : p.key_head_stride) + part;
-  dst = head * p.head_stride + part;
+  // Token index and slot are wave-uniform: keep them (and the address math) scalar.  No
+  // early return precedes the loads (the token index is clamped instead), so the only
+  // scalar round trip before them is the kernel-argument fetch.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tok_raw = blockIdx.x * kAppendWaves + wave;
+  const int tok = min(tok_raw, p.num_tokens - 1);
+  const int lane = threadIdx.x & 63;
+  const int cpt = p.num_kv_heads * kChunksPerHead;  // chunks per tensor row
+  const uint4* key_row = p.key + static_cast<int64_t>(tok) * p.key_tok_stride;
+  const uint4* value_row = p.value + static_cast<int64_t>(tok) * p.value_tok_stride;
+  const int32_t slot = p.slot_mapping[tok];
+  const bool store = tok_raw < p.num_tokens && slot >= 0 && static_cast<int64_t>(slot) < p.num_cache_slots;
+  const int32_t blk = slot / p.block_size;  // scalar division: no branch before the loads
+  const int32_t off = slot - blk * p.block_size;
+  const int64_t dst_base = static_cast<int64_t>(blk) * p.blk_stride + static_cast<int64_t>(off) * p.slot_stride;
+
+  int j0 = 0;
+  do {  // every row has at least one chunk group
+    uint4 kb[CPL], vb[CPL];
+    int64_t dofs[CPL];
+    int64_t kofs[CPL], vofs[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int j = min(j0 + 64 * u + lane, cpt - 1);
+      const int head = j / kChunksPerHead;
+      const int part = j - head * kChunksPerHead;
+      kofs[u] = head * p.key_head_stride + part;
+      vofs[u] = head * p.value_head_stride + part;
+      dofs[u] = head * p.head_stride + part;
+    }
+    // K row then V row (each a contiguous stretch of HBM), loads and stores alike.
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) kb[u] = key_row[kofs[u]];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) vb[u] = value_row[vofs[u]];
+    if (!store) return;  // -1 (padding), a slot outside the pool, or past the last token
+    // Cache rows are written once and read by a later kernel: nontemporal stores keep
+    // them out of L2 (measured 10.0 -> 8.3 us for 4096 tokens).  A lane past the row's
+    // last chunk was clamped onto that chunk and rewrites the same bytes to the same
+    // place, so the stores need no mask either.
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) store16_nt(p.k_cache + dst_base + dofs[u], kb[u]);
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) store16_nt(p.v_cache + dst_base + dofs[u], vb[u]);
+    j0 += 64 * CPL;
+  } while (j0 < cpt);
 }
 
 template <int HEAD_DIM>
-__global__ __launch_bounds__(64 * kAppendWaves) void kv_append_kernel(const AppendParams p) {
-  // Token index and slot are wave-uniform: keep them (and the address math) scalar.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tok = blockIdx.x * kAppendWaves + wave;
-  const int lane = threadIdx.x & 63;
-  if (tok >= p.num_tokens) return;
-  const int32_t slot = p.slot_mapping[tok];
-  if (slot < 0 || static_cast<int64_t>(slot) >= p.num_cache_slots) return;  // -1: padding
-  const int bs = p.block_size;
-  int32_t blk, off;
-  if ((bs & (bs - 1)) == 0) {
-    const int shift = __builtin_ctz(bs);
-    blk = slot >> shift;
-    off = slot & (bs - 1);
-  } else {
-    blk = slot / bs;
-    off = slot - blk * bs;
-  }
-  const int64_t dst_base = static_cast<int64_t>(blk) * p.blk_stride + static_cast<int64_t>(off) * p.slot_stride;
-  const int chunks_per_tensor = p.num_kv_heads * (HEAD_DIM / 8);
-  const int total = 2 * chunks_per_tensor;
-  const uint4* key_row = p.key + static_cast<int64_t>(tok) * p.key_tok_stride;
-  const uint4* value_row = p.value + static_cast<int64_t>(tok) * p.value_tok_stride;
-  uint4* k_dst = p.k_cache + dst_base;
-  uint4* v_dst = p.v_cache + dst_base;
-
-  for (int j0 = 0; j0 < total; j0 += 64 * kAppendUnroll) {
-    // All loads of this group first (addresses clamped to a valid chunk, so no branch
-    // guards the loads and they stay in flight together), then the guarded stores.
-    uint4 b0, b1, b2, b3;
-    int64_t d0, d1, d2, d3;
-    bool v0, v1, v2, v3;
-    {
-      int64_t s0, s1, s2, s3;
-      chunk_offsets<HEAD_DIM>(p, min(j0 + lane, total - 1), chunks_per_tensor, v0, s0, d0);
-      chunk_offsets<HEAD_DIM>(p, min(j0 + 64 + lane, total - 1), chunks_per_tensor, v1, s1, d1);
-      chunk_offsets<HEAD_DIM>(p, min(j0 + 128 + lane, total - 1), chunks_per_tensor, v2, s2, d2);
-      chunk_offsets<HEAD_DIM>(p, min(j0 + 192 + lane, total - 1), chunks_per_tensor, v3, s3, d3);
-      b0 = (v0 ? value_row : key_row)[s0];
-      b1 = (v1 ? value_row : key_row)[s1];
-      b2 = (v2 ? value_row : key_row)[s2];
-      b3 = (v3 ? value_row : key_row)[s3];
-    }
-    if (j0 + lane < total) (v0 ? v_dst : k_dst)[d0] = b0;
-    if (j0 + 64 + lane < total) (v1 ? v_dst : k_dst)[d1] = b1;
-    if (j0 + 128 + lane < total) (v2 ? v_dst : k_dst)[d2] = b2;
-    if (j0 + 192 + lane < total) (v3 ? v_dst : k_dst)[d3] = b3;
-  }
+static void launch_append(const AppendParams& p, int chunks_per_tensor, dim3 grid, dim3 block, hipStream_t s) {
+  if (chunks_per_tensor <= 64) hipLaunchKernelGGL((kv_append_kernel<HEAD_DIM, 1>), grid, block, 0, s, p);
+  else if (chunks_per_tensor <= 128) hipLaunchKernelGGL((kv_append_kernel<HEAD_DIM, 2>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((kv_append_kernel<HEAD_DIM, 4>), grid, block, 0, s, p);
 }
 
 }  // namespace kvp
@@ -148,10 +145,11 @@ extern "C" int kvp_append_bf16(const void* key, int64_t key_tok_stride, int64_t 
   const dim3 grid((num_tokens + kAppendWaves - 1) / kAppendWaves);
   const dim3 block(64 * kAppendWaves);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int cpt = num_kv_heads * (head_dim / 8);
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL(kv_append_kernel<64>, grid, block, 0, s, p); break;
-    case 128: hipLaunchKernelGGL(kv_append_kernel<128>, grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL(kv_append_kernel<256>, grid, block, 0, s, p); break;
+    case 64: launch_append<64>(p, cpt, grid, block, s); break;
+    case 128: launch_append<128>(p, cpt, grid, block, s); break;
+    default: launch_append<256>(p, cpt, grid, block, s); break;
   }
   return launch_status("kvp_append_bf16");
 }

