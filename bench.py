@@ -211,22 +211,22 @@ def load_traffic(name: str):
 
 def profile_run(dev) -> int:
     """Fixed launch sequence for rocprofv3 counter runs: 3 plain 1 GiB copies (the
-    calibration of the byte counters), then (after warm-up launches) 10 decode steps of
-    the Qwen3-0.6B workload, 10 KV appends, 3 prefix-cached prefills and 3 decode steps
-    of the Qwen3-8B workload."""
+    calibration of the byte counters), then (after warm-up launches) 40 decode steps of
+    the Qwen3-0.6B workload, 48 KV appends (two graph replays), 6 prefix-cached prefills
+    and 8 decode steps of the Qwen3-8B workload."""
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    bench_decode(dev, 10, 3, "qwen3_0.6b")
+    bench_decode(dev, 40, 3, "qwen3_0.6b")
     torch.cuda.empty_cache()
-    bench_append(dev, 10, 3)
+    bench_append(dev, 48, 3)
     torch.cuda.empty_cache()
-    bench_prefill(dev, 3, 1)
+    bench_prefill(dev, 6, 1)
     torch.cuda.empty_cache()
-    bench_decode(dev, 3, 1, "qwen3_8b")
+    bench_decode(dev, 8, 1, "qwen3_8b")
     torch.cuda.synchronize()
     print("profile run done", flush=True)
     return 0
@@ -244,7 +244,7 @@ PROFILE_CMDS = [
 PROFILE_KERNELS = [
     ("paged_decode_qwen3_0.6b", "void kvp::paged_decode_kernel<2,", "decode_0.6b"),
     ("paged_decode_qwen3_8b", "void kvp::paged_decode_kernel<4,", "decode_8b"),
-    ("kv_append_4096tok", "void kvp::kv_append_kernel<128>", "append"),
+    ("kv_append_4096tok", "void kvp::kv_append_kernel<128", "append"),
     ("varlen_prefill_prefix_32seq", "void kvp::varlen_prefill_kernel<2, true, true>", "prefill"),
 ]
 
@@ -298,14 +298,16 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         lines = [f"# {fname}: `{name}`", "",
                  "Commands (from the repository root on the GPU host, `R=$PWD`):", "", "```"]
         lines += PROFILE_CMDS + ["```", ""]
-        lines += [f"- dispatches: {len(d_us)}; duration avg {avg_us:.2f} us, min {min(d_us):.2f}, max {max(d_us):.2f}"]
+        med_us = statistics.median(d_us)
+        lines += [f"- dispatches: {len(d_us)} (warm-up launches included); duration avg {avg_us:.2f} us, "
+                  f"median {med_us:.2f} us, min {min(d_us):.2f}, max {max(d_us):.2f}"]
         if key == "prefill":
             lines += [f"- algorithmic work: {algo[key]} flop (unmasked query-key pairs x 4 x Hq x D) "
-                      f"-> {algo[key] / avg_us / 1e6:.1f} TFLOP/s at the average duration "
-                      f"({algo[key] / avg_us / 1e6 / BF16_PEAK_TFLOPS * 100:.1f}% of 2.5 PFLOP/s dense bf16)"]
+                      f"-> {algo[key] / med_us / 1e6:.1f} TFLOP/s at the median duration "
+                      f"({algo[key] / med_us / 1e6 / BF16_PEAK_TFLOPS * 100:.1f}% of 2.5 PFLOP/s dense bf16)"]
         else:
-            lines += [f"- algorithmic bytes: {algo[key]} -> {algo[key] / avg_us / 1e3:.1f} GB/s at the average "
-                      f"duration ({algo[key] / avg_us / 1e3 / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)"]
+            lines += [f"- algorithmic bytes: {algo[key]} -> {algo[key] / med_us / 1e3:.1f} GB/s at the median "
+                      f"duration ({algo[key] / med_us / 1e3 / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)"]
         lines += [f"- FETCH_SIZE calibration: 1 GiB copy reads {copy_f:.1f} KiB -> scale {f_scale:.4f}; "
                   f"WRITE_SIZE: 1 GiB copy writes {copy_w:.1f} KiB -> scale {w_scale:.4f}",
                   f"- HBM traffic per dispatch (scaled): read {statistics.mean(fetch):.0f} B, "
@@ -314,13 +316,13 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         if key.startswith("decode") and merge_name in dur:
             m_us = [x / 1e3 for x in dur[merge_name]]
             lines += [f"- the decode's split-combining `{merge_name}` (all decode workloads): "
-                      f"avg {statistics.mean(m_us):.2f} us over {len(m_us)} dispatches"]
+                      f"median {statistics.median(m_us):.2f} us over {len(m_us)} dispatches"]
         (out_dir / f"{fname}.md").write_text("\n".join(lines) + "\n")
         if key == "decode_0.6b":
             (out_dir / "paged_decode_qwen3_0.6b_pmc.json").write_text(json.dumps(
                 {"kernel": name, "traffic_bytes": int(round(traffic)), "fetch_scale": f_scale,
-                 "write_scale": w_scale, "avg_duration_us": avg_us}, indent=1) + "\n")
-        print(f"{fname}: {avg_us:.2f} us, traffic {traffic:.0f} B", flush=True)
+                 "write_scale": w_scale, "median_duration_us": med_us}, indent=1) + "\n")
+        print(f"{fname}: median {med_us:.2f} us, traffic {traffic:.0f} B", flush=True)
     return 0
 
 

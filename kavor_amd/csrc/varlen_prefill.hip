@@ -8,7 +8,8 @@
 // bottom-right aligned (flash-attn >= 2.1; the reference pins 2.8.3.post2, setup.py:10).
 //
 // Tiling (gfx950, wave64, v_mfma_f32_32x32x16_bf16)
-//   A workgroup (4 waves) owns one (sequence, kv head, query tile) and all G query heads
+//   A workgroup (4 waves, two resident per CU) owns one (sequence, kv head, query tile)
+//   and all G query heads
 //   of that kv head: 128 "rows" = 128/G query tokens x G heads, row rho = tok*G + g, so a
 //   staged K/V tile feeds G heads.  Wave w owns rows [32w, 32w+32).
 //   Per 64-key tile the workgroup stages K and V row-major in LDS (double-buffered, one
@@ -32,6 +33,9 @@ namespace kvp {
 
 constexpr int kPrefillHeadDim = 128;
 constexpr int kPrefillWaves = 4;
+constexpr int kPrefillThreads = 64 * kPrefillWaves;
+// 16-byte chunks of one 64-key tile (64 keys x 16 chunks) per thread, per tensor
+constexpr int kStageIters = 64 * 16 / kPrefillThreads;
 constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows (token x head) per workgroup
 constexpr int kKeyTile = 64;
 constexpr int kKStride = kPrefillHeadDim + 8;  // LDS row pitch of the K tile (bf16)
@@ -78,8 +82,12 @@ __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+// Two workgroups per CU (2 waves per SIMD, <= 256 registers per wave): the workgroups'
+// barriers are independent, so one's MFMAs overlap the other's softmax (measured
+// 1.45 -> 0.83 ms on the prefix-cached prefill workload vs one 4-wave workgroup per CU,
+// 0.97 ms with one 8-wave workgroup).
 template <int G, bool PAGED, bool CAUSAL>
-__global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2))) void varlen_prefill_kernel(const PrefillParams p) {
   constexpr int D = kPrefillHeadDim;
   constexpr int TOK = kPrefillRows / G;  // query tokens per tile
 
@@ -115,9 +123,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
   if (tid == 0) s_bad = 0;  // sticky for the workgroup: one sequence, one block table
   __syncthreads();
 
-  // Thread t stages 16-byte chunk (t % 16) of keys t/16 + 16u, u = 0..3, of a 64-key tile.
+  // Thread t stages 16-byte chunk (t % 16) of keys t/16 + (threads/16)*u of a 64-key tile.
   const int chunk = tid & 15;
-  auto load_tile = [&](int kv0, uint4 (&kc)[4], uint4 (&vc)[4]) {
+  auto load_tile = [&](int kv0, uint4 (&kc)[kStageIters], uint4 (&vc)[kStageIters]) {
     int64_t kbase = 0, vbase = 0;
     bool blk_ok = true;
     if (PAGED) {
@@ -138,8 +146,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
     kbase += static_cast<int64_t>(kvh) * p.k_head_stride + 8 * chunk;
     vbase += static_cast<int64_t>(kvh) * p.v_head_stride + 8 * chunk;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int key = (tid >> 4) + 16 * u;
+    for (int u = 0; u < kStageIters; ++u) {
+      const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
       const bool ok = kv0 + key < klen && blk_ok;
       kc[u] = ok ? *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride) : make_uint4(0, 0, 0, 0);
       vc[u] = ok ? *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride) : make_uint4(0, 0, 0, 0);
@@ -191,15 +199,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
     // smallest row_limit over this wave's rows (its first query token)
     const int wave_min_limit = CAUSAL ? q0 + (32 * wave) / G + diag : klen - 1;
 
-    uint4 kc[4], vc[4];
+    uint4 kc[kStageIters], vc[kStageIters];
     if (nkv > 0) load_tile(0, kc, vc);
     for (int it = 0; it < nkv; ++it) {
       const int kv0 = it * kKeyTile;
       uint16_t* sk = s_k[it & 1];
       uint16_t* sv = s_v[it & 1];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int key = (tid >> 4) + 16 * u;
+      for (int u = 0; u < kStageIters; ++u) {
+        const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
         *reinterpret_cast<uint4*>(&sk[key * kKStride + 8 * chunk]) = kc[u];
         *reinterpret_cast<uint4*>(&sv[key * kVStride + 8 * chunk]) = vc[u];
       }
@@ -311,7 +319,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(cons
 
 template <int G>
 static void launch_prefill(bool paged, bool causal, dim3 grid, hipStream_t s, const PrefillParams& p) {
-  const dim3 block(64 * kPrefillWaves);
+  const dim3 block(kPrefillThreads);
   if (paged) {
     if (causal) hipLaunchKernelGGL((varlen_prefill_kernel<G, true, true>), grid, block, 0, s, p);
     else hipLaunchKernelGGL((varlen_prefill_kernel<G, true, false>), grid, block, 0, s, p);
