@@ -1,6 +1,7 @@
 """Benchmark of the paged KV-cache path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu-baseline]
+                    [--no-e2e | --e2e-only] [--e2e-seqs N]
 
 A step is one paged-decode pass over the Qwen3-0.6B decode workload (256 sequences,
 16 query / 8 kv heads, head_dim 128, bf16, context lengths uniform over 100-2048,
@@ -14,6 +15,10 @@ Qwen3-8B decode workload (128 sequences, 32/8 heads, contexts 1024-32768, 20000-
 pool) and the prefix-cached varlen prefill (32 sequences, 100-1024 new tokens, prefixes
 of 0-4096 tokens shared by groups of 4).  `cpu_baseline` times the PyTorch-eager CPU
 restatement (gather + SDPA in bf16) on a bounded sample of the headline workload.
+`e2e_qwen3_0.6b` runs the engine end to end: 256 requests on the Qwen3-0.6B
+architecture with random bf16 weights, greedy, prompt and output lengths uniform over
+100-1024, reporting output tok/s (sum of max_tokens / wall time, prefill included) and
+decode tok/s (decode tokens / decode step time).
 """
 
 from __future__ import annotations
@@ -334,6 +339,73 @@ def _decode_algo_bytes(B, hq, lo, hi, pool_blocks, seed=0):
     return decode_bytes(ctx.tolist(), hq, 8, D, BS)
 
 
+# ----------------------------------------------------------------------------- end to end
+
+def e2e_workload(num_seqs: int = 256, seed: int = 0):
+    """Prompt / output lengths in the draw order of the reference's offline benchmark
+    (benchs/bench.py:9-19: random.seed(0), per request a length in [100, 1024] then its
+    ids, then every max_tokens in [100, 1024]), so the token counts match it
+    (sum(max_tokens) = 133966 for 256 requests).  The ids themselves are then redrawn
+    uniformly over the whole Qwen3 vocabulary (numpy, same seed)."""
+    import random
+
+    import numpy as np
+
+    random.seed(seed)
+    lengths = []
+    for _ in range(num_seqs):
+        n = random.randint(100, 1024)
+        for _ in range(n):
+            random.randint(0, 10000)
+        lengths.append(n)
+    max_tokens = [random.randint(100, 1024) for _ in range(num_seqs)]
+    rng = np.random.default_rng(seed)
+    prompts = [rng.integers(0, 151936, n).tolist() for n in lengths]
+    return prompts, max_tokens
+
+
+def bench_e2e(num_seqs: int = 256):
+    """Offline generation with the Qwen3-0.6B architecture (random bf16 weights), greedy,
+    ignore_eos, hipGraph decode, max_model_len 4096: output tok/s = sum(max_tokens) / wall."""
+    from kavor_amd.engine.llm_engine import LLM
+    from kavor_amd.sampling_params import SamplingParams
+
+    t0 = time.perf_counter()
+    llm = LLM(None, enforce_eager=False, max_model_len=4096, seed=0)
+    init_s = time.perf_counter() - t0
+    print(f"e2e: engine ready in {init_s:.1f}s ({llm.config.num_kvcache_blocks} pages, "
+          f"{len(llm.model_runner.graphs)} graphs)", file=sys.stderr, flush=True)
+    prompts, max_tokens = e2e_workload(num_seqs)
+    sps = [SamplingParams(temperature=0.0, ignore_eos=True, max_tokens=m) for m in max_tokens]
+    llm.generate([prompts[0][:16]], SamplingParams(temperature=0.0, max_tokens=4, ignore_eos=True))
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    outs = llm.generate(prompts, sps)
+    wall = time.perf_counter() - t
+    print(f"e2e: generated {sum(max_tokens)} tokens in {wall:.2f}s", file=sys.stderr, flush=True)
+    assert [len(o["token_ids"]) for o in outs] == max_tokens
+    s = llm.throughput_summary()
+    runner = llm.model_runner
+    res = dict(
+        output_tok_s=round(sum(max_tokens) / wall, 1),
+        decode_tok_s=round(s["decode_tok_s"], 1),
+        wall_s=round(wall, 3),
+        output_tokens=sum(max_tokens), prompt_tokens=sum(len(p) for p in prompts),
+        decode_steps=s["decode_steps"], decode_time_s=round(s["decode_time_s"], 3),
+        prefill_steps=s["prefill_steps"], prefill_time_s=round(s["prefill_time_s"], 3),
+        prefill_tok_s=round(s["prefill_tok_s"], 1),
+        num_kvcache_blocks=llm.config.num_kvcache_blocks, graphs=len(runner.graphs),
+        init_s=round(init_s, 2), capture_s=round(runner.timings["capture"], 2),
+        workload=f"{num_seqs} requests, prompt U[100,1024] ids uniform over 151936, output U[100,1024], "
+                 "greedy, ignore_eos, Qwen3-0.6B arch random bf16 weights, max_model_len 4096, "
+                 "hipGraph decode, block 256",
+    )
+    llm.exit()
+    del llm
+    torch.cuda.empty_cache()
+    return res
+
+
 # ----------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -343,6 +415,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="headline decode workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen3-0.6B generation")
+    ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end generation (prints its JSON)")
+    ap.add_argument("--e2e-seqs", type=int, default=256)
     ap.add_argument("--summarize", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/*.md (and the decode traffic json) from the CSV output of "
                          "three rocprofv3 runs of --profile: --kernel-trace --stats, --pmc "
@@ -366,6 +441,9 @@ def main() -> int:
     lib()
     if args.profile:
         return profile_run(dev)
+    if args.e2e_only:
+        print(json.dumps({"e2e_qwen3_0.6b": bench_e2e(args.e2e_seqs)}), flush=True)
+        return 0
 
     inp, dec = bench_decode(dev, args.steps, args.warmup, "qwen3_0.6b")
     extras = {}
@@ -385,6 +463,10 @@ def main() -> int:
                                                workload="B=128, 32q/8kv, ctx U[1024,32768], pool 20000 blocks")
         torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(inp)
+    if not args.no_e2e:
+        del inp
+        torch.cuda.empty_cache()
+        extras["e2e_qwen3_0.6b"] = bench_e2e(args.e2e_seqs)
 
     gbs = dec["gbs"]
     line = {

@@ -6,3 +6,18 @@ kavor/layers/attention/flash_attention_kvcache.py.
 """
 
 __version__ = "0.1.0"
+
+__all__ = ["LLM", "SamplingParams"]
+
+
+def __getattr__(name):
+    # lazy, so that importing the package (e.g. for the C-ABI binding) stays light
+    if name == "LLM":
+        from kavor_amd.engine.llm_engine import LLM
+
+        return LLM
+    if name == "SamplingParams":
+        from kavor_amd.sampling_params import SamplingParams
+
+        return SamplingParams
+    raise AttributeError(name)

@@ -1,0 +1,1 @@
+"""Engine host around the paged KV path: sequences, pages, scheduling, model runner."""
