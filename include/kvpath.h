@@ -151,6 +151,75 @@ int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int64_t q_head_
                             void* out, int64_t out_tok_stride, int64_t out_head_stride,
                             void* stream);
 
+/* ------------------------------------------------------------------------------
+ * The layer work on either side of the path (the engine's Qwen3 layers).  Same
+ * conventions as above.
+ * ------------------------------------------------------------------------------ */
+
+/*
+ * RMSNorm over rows of a bf16 view: row (t, h), t < num_tokens, h < rows_per_token,
+ * starts at x + t*x_stride0 + h*x_stride1 and has `cols` elements (a multiple of 8,
+ * at most 8192).  With residual == NULL:
+ *   out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)
+ * (replaces RMSNorm.rms_forward / _rmsnorm_kernel, kavor/layers/layernorm.py:8-40,
+ * 235-258).  With a residual (same indexing) the row is first summed in fp32,
+ *   s = x + residual;  residual <- bf16(s);  out = bf16(bf16(s * rsqrt(mean(s^2)+eps)) * weight)
+ * (replaces add_rms_forward / _add_rmsnorm_kernel, layernorm.py:113-140, 260-284; the
+ * residual is updated in place as there).  out may alias x.
+ */
+int kvp_rmsnorm_bf16(const void* x, int64_t x_stride0, int64_t x_stride1,
+                     void* residual, int64_t residual_stride0, int64_t residual_stride1,
+                     const void* weight, float eps,
+                     void* out, int64_t out_stride0, int64_t out_stride1,
+                     int32_t num_tokens, int32_t rows_per_token, int32_t cols, void* stream);
+
+/*
+ * Fused per-token q/k RMSNorm + neox RoPE + KV append for head_dim 128.  Row t of qkv
+ * holds num_q_heads q heads, then num_kv_heads k heads, then num_kv_heads v heads, each
+ * head_dim contiguous elements (the fused qkv projection output, kavor/models/qwen3.py:80-88).
+ * For each token:
+ *   q_h = rope(rmsnorm(q_h, q_norm_weight))  written to q_out + t*q_out_tok_stride + h*128
+ *   k_h = rope(rmsnorm(k_h, k_norm_weight))  written to the K cache at slot_mapping[t]
+ *   v_h                                       copied bit for bit to the V cache there
+ * rmsnorm is kvp_rmsnorm_bf16's formula; rope rotates pairs (x_i, x_{i+64}) of the bf16
+ * normalised head by cos_sin[positions[t]] (a [max_position, 128] fp32 table holding
+ * cos(p * theta_i) in columns 0..63 and sin in 64..127), in fp32, rounded once
+ * (rotary_embedding.py:8-53, 104-120).  Cache addressing and slot semantics are
+ * kvp_append_bf16's (slot -1 or outside [0, num_cache_slots) skips the token's k and v).
+ * slot_mapping may be NULL (no append; the caches are then not touched).  A position
+ * outside [0, max_position) makes that token's q and k NaN.  Replaces qwen3.py:85-89
+ * (q_norm, k_norm, rotary_emb, then Attention's store_kvcache).
+ */
+int kvp_qk_norm_rope_append_bf16(const void* qkv, int64_t qkv_tok_stride,
+                                 const int32_t* positions, const float* cos_sin,
+                                 int32_t max_position,
+                                 const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                 void* q_out, int64_t q_out_tok_stride,
+                                 void* k_cache, void* v_cache,
+                                 int64_t cache_block_stride, int64_t cache_slot_stride,
+                                 int64_t cache_head_stride, int64_t num_cache_slots,
+                                 const int32_t* slot_mapping, int32_t num_tokens,
+                                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                 int32_t block_size, void* stream);
+
+/*
+ * out[t, i] = bf16(silu(gate[t, i]) * up[t, i]) with gate = gate_up[t, 0:intermediate],
+ * up = gate_up[t, intermediate:2*intermediate], computed in fp32 and rounded once
+ * (SiluAndMul, kavor/layers/activation.py:6-11, under torch.compile).  intermediate is a
+ * multiple of 8.
+ */
+int kvp_silu_mul_bf16(const void* gate_up, int64_t gate_up_tok_stride, void* out,
+                      int64_t out_tok_stride, int32_t num_tokens, int32_t intermediate,
+                      void* stream);
+
+/*
+ * Greedy sampling: out[r] = index of the largest of logits[r, 0:vocab] (int64), the first
+ * one on ties, NaN counting as largest (torch.argmax semantics).  Replaces the
+ * temperature-0 branch of _sample_kernel (kavor/layers/sampler.py:7-45).
+ */
+int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t num_rows, int32_t vocab,
+                    int64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,7 +18,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC_DIR = PKG_DIR / "csrc"
 INCLUDE_DIR = REPO_DIR / "include"
 LIB_PATH = PKG_DIR / "libkvpath.so"
-SOURCES = ["capi.hip", "kv_append.hip", "paged_decode.hip", "varlen_prefill.hip"]
+SOURCES = ["capi.hip", "kv_append.hip", "paged_decode.hip", "varlen_prefill.hip", "norm_rope.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

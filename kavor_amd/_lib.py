@@ -62,6 +62,33 @@ SIGNATURES: dict[str, tuple] = {
         _c_void_p, _i64, _i64,            # out, out_tok_stride, out_head_stride
         _c_void_p,                        # stream
     ]),
+    "kvp_rmsnorm_bf16": (ctypes.c_int, [
+        _c_void_p, _i64, _i64,            # x, x_stride0, x_stride1
+        _c_void_p, _i64, _i64,            # residual, residual_stride0, residual_stride1
+        _c_void_p, _f32,                  # weight, eps
+        _c_void_p, _i64, _i64,            # out, out_stride0, out_stride1
+        _i32, _i32, _i32,                 # num_tokens, rows_per_token, cols
+        _c_void_p,                        # stream
+    ]),
+    "kvp_qk_norm_rope_append_bf16": (ctypes.c_int, [
+        _c_void_p, _i64,                  # qkv, qkv_tok_stride
+        _c_void_p, _c_void_p, _i32,       # positions, cos_sin, max_position
+        _c_void_p, _c_void_p, _f32,       # q_norm_weight, k_norm_weight, eps
+        _c_void_p, _i64,                  # q_out, q_out_tok_stride
+        _c_void_p, _c_void_p,             # k_cache, v_cache
+        _i64, _i64, _i64, _i64,           # cache block/slot/head strides, num_cache_slots
+        _c_void_p, _i32,                  # slot_mapping, num_tokens
+        _i32, _i32, _i32, _i32,           # num_q_heads, num_kv_heads, head_dim, block_size
+        _c_void_p,                        # stream
+    ]),
+    "kvp_silu_mul_bf16": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _i64,  # gate_up, gate_up_tok_stride, out, out_tok_stride
+        _i32, _i32, _c_void_p,            # num_tokens, intermediate, stream
+    ]),
+    "kvp_argmax_bf16": (ctypes.c_int, [
+        _c_void_p, _i64, _i32, _i32,      # logits, row_stride, num_rows, vocab
+        _c_void_p, _c_void_p,             # out (int64), stream
+    ]),
 }
 
 _lock = threading.Lock()

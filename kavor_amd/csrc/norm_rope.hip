@@ -1,0 +1,417 @@
+// The layer work on either side of the paged KV path, fused for gfx950:
+//
+//   rmsnorm_kernel            (add-)RMSNorm over rows of any 2-D or [T, H, D] strided view
+//                             (kavor/layers/layernorm.py:8-40, 113-140, 235-284)
+//   qk_norm_rope_append_kernel  per token: q/k RMSNorm, neox RoPE, q written out, k and v
+//                             appended to the paged cache (qwen3.py:79-89,
+//                             rotary_embedding.py:8-53, flash_attention_kvcache.py:10-34)
+//   silu_mul_kernel           SiLU(gate) * up (kavor/layers/activation.py:6-11)
+//   argmax_kernel             greedy token per logits row (kavor/layers/sampler.py:7-45, T = 0)
+//
+// All are HBM / latency bound elementwise work: every thread moves 16-byte vectors of 8
+// bf16, reductions stay in registers (DPP inside a 16-lane row, lane swaps across rows),
+// nothing goes through LDS except the argmax's cross-wave step.  Numerics follow the
+// reference's eager formulas: statistics in fp32, the normalised value rounded to bf16
+// before the weight multiply (double rounding, layernorm.py:32-33), RoPE rotated in fp32
+// and rounded once.
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace kvp {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ void unpack8(const uint4 w, float f[8]) {
+  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+__device__ __forceinline__ uint4 pack8(const float f[8]) {
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
+                    pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
+// Rounds to bf16 and back (the eager path's intermediate bf16 tensors).
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float(static_cast<u32>(f32_to_bf16(x)) << 16);
+}
+
+__device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void store16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+// ------------------------------------------------------------------ RMSNorm
+
+struct NormParams {
+  const uint16_t* x;
+  int64_t x_s0, x_s1;          // row (t, h) starts at x + t*x_s0 + h*x_s1 (elements)
+  uint16_t* residual;          // nullptr: plain RMSNorm; else read, added, rewritten in place
+  int64_t r_s0, r_s1;
+  const uint16_t* weight;
+  uint16_t* out;
+  int64_t o_s0, o_s1;
+  int rows_inner;              // rows per leading index (H of a [T, H, D] view, 1 for 2-D)
+  int num_rows;
+  int cols;                    // multiple of 8
+  float eps;
+};
+
+// LANES (16 or 64) lanes normalise one row; each lane owns up to MAXC 8-element chunks.
+template <int LANES, int MAXC>
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(NormParams p) {
+  const int lane = threadIdx.x % LANES;
+  const int row = (blockIdx.x * kThreads + threadIdx.x) / LANES;
+  if (row >= p.num_rows) return;  // uniform across the lanes of a row
+  const int t = row / p.rows_inner, h = row - t * p.rows_inner;
+  const uint16_t* xr = p.x + t * p.x_s0 + h * p.x_s1;
+  uint16_t* rr = p.residual ? p.residual + t * p.r_s0 + h * p.r_s1 : nullptr;
+  uint16_t* orow = p.out + t * p.o_s0 + h * p.o_s1;
+  const int nch = p.cols >> 3;
+
+  float v[MAXC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = lane + i * LANES;
+    const bool ok = c < nch;
+    const int cc = ok ? c : 0;
+    unpack8(load16(xr + 8 * cc), v[i]);
+    if (rr) {
+      float r[8];
+      unpack8(load16(rr + 8 * cc), r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[i][e] += r[e];
+      if (ok) store16(rr + 8 * c, pack8(v[i]));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (!ok) v[i][e] = 0.f;
+      ss += v[i][e] * v[i][e];
+    }
+  }
+  ss = row16_sum(ss);
+  if (LANES == 64) {
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+  }
+  const float rstd = rsqrtf(ss / static_cast<float>(p.cols) + p.eps);
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = lane + i * LANES;
+    if (c < nch) {
+      float w[8], y[8];
+      unpack8(load16(p.weight + 8 * c), w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = round_bf16(v[i][e] * rstd) * w[e];
+      store16(orow + 8 * c, pack8(y));
+    }
+  }
+}
+
+template <int LANES, int MAXC>
+void launch_norm(const NormParams& p, hipStream_t stream) {
+  const int rows_per_block = kThreads / LANES;
+  const int grid = (p.num_rows + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((rmsnorm_kernel<LANES, MAXC>), dim3(grid), dim3(kThreads), 0, stream, p);
+}
+
+// ------------------------------------------------------------------ q/k norm + RoPE + append
+
+constexpr int kRopeDim = 128;  // head_dim of the fused kernel: 16 lanes x 8 elements
+
+struct QkParams {
+  const uint16_t* qkv;
+  int64_t qkv_stride;          // token row stride; heads are consecutive D-element blocks
+  const int32_t* positions;
+  const float* cos_sin;        // [max_position, D] fp32: cos of the D/2 frequencies, then sin
+  int max_position;
+  const uint16_t* q_weight;
+  const uint16_t* k_weight;
+  float eps;
+  uint16_t* q_out;
+  int64_t q_out_stride;        // token stride of q_out; heads D apart
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t blk_stride, slot_stride, head_stride, num_cache_slots;
+  const int32_t* slot_mapping;
+  int num_tokens, hq, hkv, block_size;
+};
+
+// One 16-lane row handles one head of one token: rows [0, hq) are q heads, [hq, hq+hkv)
+// k heads, [hq+hkv, hq+2hkv) v heads.  Lane j of the row holds elements 8j..8j+7; the RoPE
+// partner of element i (< 64) is i + 64, which lives in lane j ^ 8 (DPP row_ror:8).
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(QkParams p) {
+  const int lane = threadIdx.x & 15;
+  const int heads = p.hq + 2 * p.hkv;
+  const int64_t grow = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4);
+  if (grow >= static_cast<int64_t>(p.num_tokens) * heads) return;  // uniform across the row
+  const int t = static_cast<int>(grow / heads);
+  const int r = static_cast<int>(grow - static_cast<int64_t>(t) * heads);
+  const uint4 raw = load16(p.qkv + t * p.qkv_stride + r * kRopeDim + 8 * lane);
+
+  const int slot = p.slot_mapping ? p.slot_mapping[t] : -1;
+  const bool store_kv = slot >= 0 && slot < p.num_cache_slots;
+  int64_t cache_off = 0;
+  if (store_kv) {
+    const int blk = slot / p.block_size, off = slot - blk * p.block_size;
+    cache_off = blk * p.blk_stride + off * p.slot_stride + 8 * lane;
+  }
+  if (r >= p.hq + p.hkv) {  // v head: bit copy into the cache
+    if (store_kv) store16(p.v_cache + cache_off + (r - p.hq - p.hkv) * p.head_stride, raw);
+    return;
+  }
+  const bool is_q = r < p.hq;
+  if (!is_q && !store_kv) return;  // k head of a padding token (uniform across the row)
+  float x[8], w[8];
+  unpack8(raw, x);
+  unpack8(load16((is_q ? p.q_weight : p.k_weight) + 8 * lane), w);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = row16_sum(ss);
+  const float rstd = rsqrtf(ss * (1.0f / kRopeDim) + p.eps);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = round_bf16(round_bf16(x[e] * rstd) * w[e]);
+
+  // partner half: the same 8 elements of lane ^ 8
+  uint4 mine = pack8(x), other;
+  other.x = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.x), 0x128, 0xf, 0xf, false));
+  other.y = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.y), 0x128, 0xf, 0xf, false));
+  other.z = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.z), 0x128, 0xf, 0xf, false));
+  other.w = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.w), 0x128, 0xf, 0xf, false));
+  float y[8];
+  unpack8(other, y);
+
+  int pos = p.positions[t];
+  const bool pos_ok = pos >= 0 && pos < p.max_position;
+  pos = pos_ok ? pos : 0;
+  const int fi = 8 * (lane & 7);  // frequency index of this lane's first element
+  const float* cs = p.cos_sin + static_cast<int64_t>(pos) * kRopeDim;
+  float c[8], s[8];
+  *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(cs + fi);
+  *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(cs + fi + 4);
+  *reinterpret_cast<float4*>(s) = *reinterpret_cast<const float4*>(cs + kRopeDim / 2 + fi);
+  *reinterpret_cast<float4*>(s + 4) = *reinterpret_cast<const float4*>(cs + kRopeDim / 2 + fi + 4);
+  const bool first_half = lane < 8;
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // first half: x1*cos - x2*sin; second half: x2*cos + x1*sin
+    o[e] = first_half ? x[e] * c[e] - y[e] * s[e] : x[e] * c[e] + y[e] * s[e];
+    if (!pos_ok) o[e] = __builtin_nanf("");
+  }
+  const uint4 packed = pack8(o);
+  if (is_q) {
+    store16(p.q_out + t * p.q_out_stride + r * kRopeDim + 8 * lane, packed);
+  } else if (store_kv) {
+    store16(p.k_cache + cache_off + (r - p.hq) * p.head_stride, packed);
+  }
+}
+
+// ------------------------------------------------------------------ SiLU * up
+
+struct SiluParams {
+  const uint16_t* gate_up;     // row t: [gate (inter) | up (inter)]
+  int64_t gu_stride;
+  uint16_t* out;
+  int64_t out_stride;
+  int num_tokens, inter;
+};
+
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(SiluParams p) {
+  const int per_row = p.inter >> 3;
+  const int64_t total = static_cast<int64_t>(p.num_tokens) * per_row;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int t = static_cast<int>(i / per_row);
+    const int c = static_cast<int>(i - static_cast<int64_t>(t) * per_row);
+    const uint16_t* row = p.gate_up + t * p.gu_stride + 8 * c;
+    float g[8], u[8], o[8];
+    unpack8(load16(row), g);
+    unpack8(load16(row + p.inter), u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
+    store16(p.out + t * p.out_stride + 8 * c, pack8(o));
+  }
+}
+
+// ------------------------------------------------------------------ argmax
+
+constexpr int kArgmaxThreads = 1024;
+
+struct ArgmaxParams {
+  const uint16_t* logits;
+  int64_t row_stride;
+  int vocab;
+  int64_t* out;
+};
+
+// (v, i) beats (b, j): NaN above every number (as torch.argmax), then larger value, then
+// the smaller index on ties (first occurrence).
+__device__ __forceinline__ bool beats(float v, int i, float b, int j) {
+  const bool vn = v != v, bn = b != b;
+  if (vn || bn) return vn && (!bn || i < j);
+  return v > b || (v == b && i < j);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(ArgmaxParams p) {
+  const uint16_t* row = p.logits + blockIdx.x * p.row_stride;
+  float best = -__builtin_inff();
+  int bi = 0x7fffffff;
+  const int nvec = p.vocab >> 3;
+  for (int c = threadIdx.x; c < nvec; c += kArgmaxThreads) {
+    float f[8];
+    unpack8(load16_nt(row + 8 * c), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (beats(f[e], 8 * c + e, best, bi)) { best = f[e]; bi = 8 * c + e; }
+  }
+  const int tail = p.vocab - 8 * nvec;
+  if (static_cast<int>(threadIdx.x) < tail) {
+    const int i = 8 * nvec + threadIdx.x;
+    const float f = __uint_as_float(static_cast<u32>(row[i]) << 16);
+    if (beats(f, i, best, bi)) { best = f; bi = i; }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ob = __shfl_xor(best, off);
+    const int oi = __shfl_xor(bi, off);
+    if (beats(ob, oi, best, bi)) { best = ob; bi = oi; }
+  }
+  __shared__ float s_best[kArgmaxThreads / 64];
+  __shared__ int s_idx[kArgmaxThreads / 64];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { s_best[wave] = best; s_idx[wave] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxThreads / 64; ++w)
+      if (beats(s_best[w], s_idx[w], best, bi)) { best = s_best[w]; bi = s_idx[w]; }
+    p.out[blockIdx.x] = bi;
+  }
+}
+
+}  // namespace
+}  // namespace kvp
+
+using namespace kvp;
+
+extern "C" int kvp_rmsnorm_bf16(const void* x, int64_t x_stride0, int64_t x_stride1,
+                                void* residual, int64_t residual_stride0, int64_t residual_stride1,
+                                const void* weight, float eps,
+                                void* out, int64_t out_stride0, int64_t out_stride1,
+                                int32_t num_tokens, int32_t rows_per_token, int32_t cols,
+                                void* stream) {
+  clear_error();
+  if (!x || !weight || !out) return fail(KVP_EINVAL, "null pointer");
+  if (num_tokens < 0 || rows_per_token < 1 || cols < 8 || cols % 8 != 0)
+    return fail(KVP_EINVAL, "bad shape: num_tokens=%d rows_per_token=%d cols=%d (cols must be a "
+                "positive multiple of 8)", num_tokens, rows_per_token, cols);
+  if (cols > 64 * 8 * 16)
+    return fail(KVP_EUNSUPPORTED, "cols=%d exceeds the supported maximum of 8192", cols);
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out) || (residual && !aligned16(residual)))
+    return fail(KVP_EINVAL, "pointers must be 16-byte aligned");
+  if (!mult8(x_stride0) || !mult8(x_stride1) || !mult8(out_stride0) || !mult8(out_stride1) ||
+      (residual && (!mult8(residual_stride0) || !mult8(residual_stride1))))
+    return fail(KVP_EINVAL, "strides must be multiples of 8 elements");
+  const int64_t rows = static_cast<int64_t>(num_tokens) * rows_per_token;
+  if (rows > INT32_MAX / 64) return fail(KVP_EINVAL, "too many rows (%lld)", (long long)rows);
+  if (rows == 0) return KVP_OK;
+  NormParams p{static_cast<const uint16_t*>(x), x_stride0, x_stride1,
+               static_cast<uint16_t*>(residual), residual_stride0, residual_stride1,
+               static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+               out_stride0, out_stride1, rows_per_token, static_cast<int>(rows), cols, eps};
+  auto s = static_cast<hipStream_t>(stream);
+  const int nch = cols / 8;
+  if (nch <= 16) launch_norm<16, 1>(p, s);
+  else if (nch <= 128) launch_norm<64, 2>(p, s);
+  else if (nch <= 256) launch_norm<64, 4>(p, s);
+  else if (nch <= 512) launch_norm<64, 8>(p, s);
+  else launch_norm<64, 16>(p, s);
+  return launch_status("rmsnorm_kernel");
+}
+
+extern "C" int kvp_qk_norm_rope_append_bf16(
+    const void* qkv, int64_t qkv_tok_stride, const int32_t* positions, const float* cos_sin,
+    int32_t max_position, const void* q_norm_weight, const void* k_norm_weight, float eps,
+    void* q_out, int64_t q_out_tok_stride,
+    void* k_cache, void* v_cache, int64_t cache_block_stride, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int64_t num_cache_slots, const int32_t* slot_mapping,
+    int32_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, void* stream) {
+  clear_error();
+  if (head_dim != kRopeDim)
+    return fail(KVP_EUNSUPPORTED, "head_dim=%d: the fused q/k norm + RoPE kernel handles 128", head_dim);
+  if (!qkv || !positions || !cos_sin || !q_norm_weight || !k_norm_weight || !q_out)
+    return fail(KVP_EINVAL, "null pointer");
+  if (slot_mapping && (!k_cache || !v_cache)) return fail(KVP_EINVAL, "slot_mapping without caches");
+  if (num_tokens < 0 || num_q_heads < 1 || num_kv_heads < 1 || max_position < 1)
+    return fail(KVP_EINVAL, "bad shape");
+  if (slot_mapping && (block_size < 1 || num_cache_slots < 0))
+    return fail(KVP_EINVAL, "bad block_size / num_cache_slots");
+  if (!aligned16(qkv) || !aligned16(q_out) || !aligned16(cos_sin) || !aligned16(q_norm_weight) ||
+      !aligned16(k_norm_weight) || (slot_mapping && (!aligned16(k_cache) || !aligned16(v_cache))))
+    return fail(KVP_EINVAL, "pointers must be 16-byte aligned");
+  if (!mult8(qkv_tok_stride) || !mult8(q_out_tok_stride) ||
+      (slot_mapping && (!mult8(cache_block_stride) || !mult8(cache_slot_stride) ||
+                        !mult8(cache_head_stride))))
+    return fail(KVP_EINVAL, "strides must be multiples of 8 elements");
+  if (qkv_tok_stride < static_cast<int64_t>(num_q_heads + 2 * num_kv_heads) * head_dim)
+    return fail(KVP_EINVAL, "qkv row stride %lld is shorter than (hq + 2 hkv) * head_dim",
+                (long long)qkv_tok_stride);
+  const int64_t heads = num_q_heads + 2 * num_kv_heads;
+  const int64_t rows = static_cast<int64_t>(num_tokens) * heads;
+  if (rows == 0) return KVP_OK;
+  const int64_t grid = (rows + kThreads / 16 - 1) / (kThreads / 16);
+  if (grid > INT32_MAX) return fail(KVP_EINVAL, "too many tokens");
+  QkParams p{static_cast<const uint16_t*>(qkv), qkv_tok_stride, positions, cos_sin, max_position,
+             static_cast<const uint16_t*>(q_norm_weight), static_cast<const uint16_t*>(k_norm_weight),
+             eps, static_cast<uint16_t*>(q_out), q_out_tok_stride,
+             static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+             cache_block_stride, cache_slot_stride, cache_head_stride, num_cache_slots,
+             slot_mapping, num_tokens, num_q_heads, num_kv_heads, block_size};
+  hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return launch_status("qk_norm_rope_append_kernel");
+}
+
+extern "C" int kvp_silu_mul_bf16(const void* gate_up, int64_t gate_up_tok_stride, void* out,
+                                 int64_t out_tok_stride, int32_t num_tokens, int32_t intermediate,
+                                 void* stream) {
+  clear_error();
+  if (!gate_up || !out) return fail(KVP_EINVAL, "null pointer");
+  if (num_tokens < 0 || intermediate < 8 || intermediate % 8 != 0)
+    return fail(KVP_EINVAL, "intermediate=%d must be a positive multiple of 8", intermediate);
+  if (!aligned16(gate_up) || !aligned16(out)) return fail(KVP_EINVAL, "pointers must be 16-byte aligned");
+  if (!mult8(gate_up_tok_stride) || !mult8(out_tok_stride))
+    return fail(KVP_EINVAL, "strides must be multiples of 8 elements");
+  if (gate_up_tok_stride < 2 * static_cast<int64_t>(intermediate))
+    return fail(KVP_EINVAL, "gate_up row stride shorter than 2 * intermediate");
+  const int64_t total = static_cast<int64_t>(num_tokens) * (intermediate / 8);
+  if (total == 0) return KVP_OK;
+  const int64_t grid = std::min<int64_t>((total + kThreads - 1) / kThreads, 256 * 16);
+  SiluParams p{static_cast<const uint16_t*>(gate_up), gate_up_tok_stride, static_cast<uint16_t*>(out),
+               out_tok_stride, num_tokens, intermediate};
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return launch_status("silu_mul_kernel");
+}
+
+extern "C" int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t num_rows,
+                               int32_t vocab, int64_t* out, void* stream) {
+  clear_error();
+  if (!logits || !out) return fail(KVP_EINVAL, "null pointer");
+  if (num_rows < 0 || vocab < 1) return fail(KVP_EINVAL, "bad shape");
+  if (!aligned16(logits) || !mult8(row_stride) || row_stride < vocab)
+    return fail(KVP_EINVAL, "logits must be 16-byte aligned with a row stride >= vocab that is a "
+                "multiple of 8 elements");
+  if (num_rows == 0) return KVP_OK;
+  ArgmaxParams p{static_cast<const uint16_t*>(logits), row_stride, vocab, out};
+  hipLaunchKernelGGL(argmax_kernel, dim3(num_rows), dim3(kArgmaxThreads), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return launch_status("argmax_kernel");
+}

@@ -285,7 +285,6 @@ __device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh
 
 template <int G, int STEP>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const DecodeParams p) {
-  constexpr int D = kDecodeHeadDim;
   constexpr int NL = STEP / 4;  // dwordx4 loads per lane per tensor per step
   constexpr int kMinSteps = kMinRangeTokens / STEP;
   __shared__ int s_cum[kMaxSeqsPerLaunch + 1];

@@ -56,8 +56,10 @@ def _pinned_int32(n: int, pin: bool) -> torch.Tensor:
     return torch.empty(n, dtype=torch.int32, pin_memory=pin)
 
 
-def prefill_arrays(seqs: list[Sequence], block_size: int):
-    """Host arrays of a prefill step (numpy int32); see the module docstring."""
+def prefill_arrays(seqs: list[Sequence], block_size: int, always_tables: bool = False):
+    """Host arrays of a prefill step (numpy int32); see the module docstring.  With
+    always_tables the block tables are produced even without cached tokens (attention
+    that reads the pages for every prefill needs them)."""
     n = len(seqs)
     qlens = np.fromiter((s.num_scheduled_tokens for s in seqs), dtype=np.int64, count=n)
     starts = np.fromiter((s.num_cached_tokens for s in seqs), dtype=np.int64, count=n)
@@ -84,7 +86,7 @@ def prefill_arrays(seqs: list[Sequence], block_size: int):
     cu_q[1:] = np.cumsum(qlens)
     cu_k[1:] = np.cumsum(klens)
     tables = None
-    if int(klens.sum()) > T:
+    if always_tables or int(klens.sum()) > T:
         width = max(len(s.block_table) for s in seqs)
         tables = np.full((n, width), -1, dtype=np.int32)
         for i, s in enumerate(seqs):
@@ -94,8 +96,9 @@ def prefill_arrays(seqs: list[Sequence], block_size: int):
                 block_tables=tables)
 
 
-def prepare_prefill(seqs: list[Sequence], block_size: int, device, pin: bool = True) -> PrefillMeta:
-    a = prefill_arrays(seqs, block_size)
+def prepare_prefill(seqs: list[Sequence], block_size: int, device, pin: bool = True,
+                    always_tables: bool = False) -> PrefillMeta:
+    a = prefill_arrays(seqs, block_size, always_tables)
     parts = [a["input_ids"], a["positions"], a["slot_mapping"], a["cu_seqlens_q"], a["cu_seqlens_k"]]
     if a["block_tables"] is not None:
         parts.append(a["block_tables"].reshape(-1))

@@ -7,8 +7,8 @@ the shared-memory control plane of :85-106 has nothing to do):
 - allocate_kv_cache (:329-383): a temporary pool serves a worst-case prefill and a
   full-batch decode whose activation peaks are measured; the page pool then takes
   total * gpu_memory_utilization - used - reserve (cache_pool.py:292-307);
-- warmup_model / _profile_decode (:128-169): synthetic prefill (slot_mapping = arange)
-  and decode (all slots 0, context length 1) passes;
+- warmup_model / _profile_decode (:128-169): synthetic worst-case prefill (each
+  sequence on its own consecutive blocks) and decode (all slots 0, context length 1);
 - capture_cudagraph (:264-327): one hipGraph per batch size in
   [1, 2, 4, 8] + range(16, max_bs + 1, 16) (+ max_bs), sharing one memory pool,
   captured with all-zero metadata and including the LM head; the paged-decode
@@ -16,8 +16,10 @@ the shared-memory control plane of :85-106 has nothing to do):
 - run / run_model (:213-262): prefill runs eagerly, decode replays the smallest graph
   that holds the batch, padding rows carry slot -1 and context length 0.
 
-Per-step metadata travels in one host-to-device copy (kavor_amd.engine.metadata).
-Sampling runs after the graph: greedy batches take one argmax over the logits.
+Per-step metadata travels in one host-to-device copy (kavor_amd.engine.metadata); the
+prefill always carries block tables because the model appends k / v before attention
+and attention reads the pages.  Sampling runs after the graph: greedy batches take one
+argmax pass over the logits.
 """
 
 from __future__ import annotations
@@ -94,15 +96,18 @@ class ModelRunner:
 
     @torch.inference_mode()
     def warmup_model(self) -> None:
-        """Worst-case dense prefill; slot_mapping = arange must fit the bound pool."""
+        """Worst-case prefill: sequence i owns blocks [i*n, (i+1)*n) of the bound pool."""
         seq_len, num_seqs = self._prefill_shape()
+        nb = math.ceil(seq_len / self.block_size)
         total = seq_len * num_seqs
         dev = self.device
         ids = torch.zeros(total, dtype=torch.int32, device=dev)
-        pos = torch.arange(seq_len, dtype=torch.int32, device=dev).repeat(num_seqs)
+        p = torch.arange(seq_len, dtype=torch.int32, device=dev)
+        pos = p.repeat(num_seqs)
+        tables = torch.arange(num_seqs * nb, dtype=torch.int32, device=dev).view(num_seqs, nb)
+        slots = (tables[:, p // self.block_size] * self.block_size + p % self.block_size).reshape(-1)
         cu = torch.arange(0, total + 1, seq_len, dtype=torch.int32, device=dev)
-        slots = torch.arange(total, dtype=torch.int32, device=dev)
-        set_context(True, cu, cu, seq_len, seq_len, slots, None, None)
+        set_context(True, cu, cu, seq_len, seq_len, slots.contiguous(), None, tables)
         try:
             logits = self.model.compute_logits(self.model(ids, pos))
             self.sampler(logits, None, True)
@@ -136,7 +141,7 @@ class ModelRunner:
     def allocate_kv_cache(self) -> None:
         cfg = self.config
         seq_len, num_seqs = self._prefill_shape()
-        probe_blocks = math.ceil(seq_len * num_seqs / self.block_size) + 2
+        probe_blocks = num_seqs * math.ceil(seq_len / self.block_size) + 2
         decode_bs = min(cfg.max_num_seqs, MAX_GRAPH_BATCH)
         reserve_decode_workspace(decode_bs, self.spec.num_attention_heads, self.spec.head_dim,
                                  self.max_blocks, self.block_size, self.device)
@@ -207,7 +212,7 @@ class ModelRunner:
         all_greedy = all(t == 0.0 for t in temps)
         try:
             if is_prefill:
-                m = prepare_prefill(seqs, self.block_size, self.device)
+                m = prepare_prefill(seqs, self.block_size, self.device, always_tables=True)
                 set_context(True, m.cu_seqlens_q, m.cu_seqlens_k, m.max_seqlen_q, m.max_seqlen_k,
                             m.slot_mapping, None, m.block_tables)
                 logits = self.model.compute_logits(self.model(m.input_ids, m.positions))

@@ -1,23 +1,20 @@
 """Qwen3 decoder that drives the paged KV path end to end.
 
-The model is the caller of the path (kavor/models/qwen3.py:75-91): per layer it projects
-q/k/v, applies the per-head q/k RMSNorm and neox RoPE, and hands q, k, v to
-kavor_amd.layers.attention.Attention, which appends k/v to the page pool and runs paged
-decode or varlen prefill.  Everything else is plain PyTorch on the GPU (hipBLASLt GEMMs
-and elementwise kernels) and follows the reference's numerics:
+The model is the caller of the path (kavor/models/qwen3.py:75-91).  Per layer:
 
-- RMSNorm in fp32, rounded to bf16, then multiplied by the bf16 weight
-  (kavor/layers/layernorm.py:235-258); the fused add variant adds in fp32 and stores
-  the residual in bf16 (layernorm.py:260-284);
-- neox rotary embedding from an fp32 cos|sin table, rotated in fp32
-  (kavor/layers/rotary_embedding.py:56-120);
-- SiLU(gate) * up (kavor/layers/activation.py:6-11);
-- tied embedding / LM head; during prefill only the last token of each sequence is
-  projected to logits (kavor/layers/embed_head.py:56-66).
+  add-RMSNorm (HIP) -> qkv GEMM -> fused q/k RMSNorm + RoPE + K/V append (HIP)
+  -> paged attention over the page pool (HIP) -> o GEMM -> add-RMSNorm (HIP)
+  -> gate_up GEMM -> SiLU * up (HIP) -> down GEMM
 
-Head layout matches qwen3.py:79-88: q/k are normalised into new contiguous tensors (k
-row stride Hkv*D) while v stays a strided view of the fused qkv output (row stride
-(Hq+2Hkv)*D), which is what the append kernel is given.
+GEMMs are torch (hipBLASLt); every other op is a kernel of libkvpath.so
+(kavor_amd.layers.fused, kavor_amd.layers.attention), with the reference's numerics:
+RMSNorm statistics in fp32 and the normalised value rounded to bf16 before the weight
+(kavor/layers/layernorm.py:235-284), neox RoPE in fp32 (rotary_embedding.py:8-53), SiLU in
+fp32 (activation.py:6-11).  Because k and v go straight from the qkv rows into the
+pages, prefill attention always reads the pages (the runner always passes block
+tables), which is the reference's prefix-cache mode (flash_attention_kvcache.py:74-79)
+applied to every prefill.  The embedding / LM head are tied; during prefill only each
+sequence's last token is projected to logits (kavor/layers/embed_head.py:56-66).
 """
 
 from __future__ import annotations
@@ -31,6 +28,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from kavor_amd.layers import fused
 from kavor_amd.layers.attention import Attention
 from kavor_amd.utils.context import get_context
 
@@ -86,31 +84,13 @@ class Qwen3Spec:
 
 # ------------------------------------------------------------------ layers
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)
-    return xf.to(x.dtype) * weight
-
-
-def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
-    xf = x.float() + residual.float()
-    residual = xf.to(x.dtype)
-    xf = xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)
-    return xf.to(x.dtype) * weight, residual
-
-
 def rope_cache(head_dim: int, max_position: int, base: float, device) -> torch.Tensor:
-    """[max_position, head_dim] fp32: cos of each frequency in the first half, sin in the second."""
+    """[max_position, head_dim] fp32: cos of each frequency in the first half, sin in the
+    second (the cos_sin_cache of rotary_embedding.py:56-66, without its head axis)."""
     inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim))
     t = torch.arange(max_position, dtype=torch.float32, device=device)
     freqs = torch.outer(t, inv_freq)
-    return torch.cat((freqs.cos(), freqs.sin()), dim=-1)
-
-
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """neox rotation of x [T, H, D] by per-token cos/sin [T, 1, D/2], computed in fp32."""
-    x1, x2 = x.float().chunk(2, dim=-1)
-    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).contiguous()
 
 
 class RMSNorm(nn.Module):
@@ -122,8 +102,8 @@ class RMSNorm(nn.Module):
 
     def forward(self, x, residual=None):
         if residual is None:
-            return rms_norm(x, self.weight, self.eps)
-        return add_rms_norm(x, residual, self.weight, self.eps)
+            return fused.rms_norm(x, self.weight, self.eps)
+        return fused.add_rms_norm(x, residual, self.weight, self.eps)
 
 
 def _weight(*shape, device, dtype) -> nn.Parameter:
@@ -148,16 +128,15 @@ class Qwen3Attention(nn.Module):
 
     def forward(self, positions: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
         qkv = F.linear(hidden, self.qkv_proj)
-        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q = self.q_norm(q.view(-1, self.num_heads, self.head_dim))
-        k = self.k_norm(k.view(-1, self.num_kv_heads, self.head_dim))
-        v = v.view(-1, self.num_kv_heads, self.head_dim)
-        cs = self.rope[positions].unsqueeze(1)
-        cos, sin = cs.chunk(2, dim=-1)
-        q = apply_rope(q, cos, sin)
-        k = apply_rope(k, cos, sin)
-        o = self.attn(q, k, v)
-        return F.linear(o.flatten(1, -1), self.o_proj)
+        attn = self.attn
+        k_cache, v_cache = attn.k_cache[0], attn.v_cache[0]
+        bound = k_cache.numel() > 0 and v_cache.numel() > 0
+        q = fused.qk_norm_rope_append(
+            qkv, positions, self.rope, self.q_norm.weight, self.k_norm.weight, self.q_norm.eps,
+            self.num_heads, self.num_kv_heads, k_cache if bound else None, v_cache if bound else None,
+            get_context().slot_mapping if bound else None)
+        o = attn.forward_cached(q)
+        return F.linear(o.reshape(q.shape[0], self.q_size), self.o_proj)
 
 
 class Qwen3MLP(nn.Module):
@@ -169,8 +148,7 @@ class Qwen3MLP(nn.Module):
         self.down_proj = _weight(spec.hidden_size, spec.intermediate_size, device=device, dtype=dtype)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gate, up = F.linear(x, self.gate_up_proj).chunk(2, dim=-1)
-        return F.linear(F.silu(gate) * up, self.down_proj)
+        return F.linear(fused.silu_and_mul(F.linear(x, self.gate_up_proj)), self.down_proj)
 
 
 class Qwen3DecoderLayer(nn.Module):

@@ -267,12 +267,30 @@ class Attention(nn.Module):
         if context.is_prefill:
             if context.block_tables is not None:  # prefix cache: attend over the pages
                 k, v = k_cache, v_cache
-            return varlen_prefill(q, k, v, max_seqlen_q=context.max_seqlen_q,
-                                  cu_seqlens_q=context.cu_seqlens_q,
-                                  max_seqlen_k=context.max_seqlen_k,
-                                  cu_seqlens_k=context.cu_seqlens_k,
-                                  softmax_scale=self.scale, causal=True,
-                                  block_table=context.block_tables)
+            return self._prefill(q, k, v, context)
+        return self._decode(q, k_cache, v_cache, context)
+
+    def forward_cached(self, q: torch.Tensor, slot: int = 0):
+        """Attention over the pages when the caller has already appended this step's k / v
+        (the fused q/k-norm + RoPE + append kernel).  Prefill then always reads the pages,
+        so the context must carry block tables."""
+        context = get_context()
+        k_cache, v_cache = self.k_cache[slot], self.v_cache[slot]
+        if context.is_prefill:
+            if context.block_tables is None:
+                raise ValueError("forward_cached prefill reads the pages: the context needs block tables")
+            return self._prefill(q, k_cache, v_cache, context)
+        return self._decode(q, k_cache, v_cache, context)
+
+    def _prefill(self, q, k, v, context):
+        return varlen_prefill(q, k, v, max_seqlen_q=context.max_seqlen_q,
+                              cu_seqlens_q=context.cu_seqlens_q,
+                              max_seqlen_k=context.max_seqlen_k,
+                              cu_seqlens_k=context.cu_seqlens_k,
+                              softmax_scale=self.scale, causal=True,
+                              block_table=context.block_tables)
+
+    def _decode(self, q, k_cache, v_cache, context):
         return paged_decode(q.unsqueeze(1), k_cache, v_cache,
                             cache_seqlens=context.context_lens,
                             block_table=context.block_tables,

@@ -1,8 +1,9 @@
 """Full-sequence fp32-attention forward of a Qwen3ForCausalLM, for checking the engine.
 
 Recomputes the logits of every position of a token sequence with the model's own
-weights and non-attention layers, but with attention as a causal fp32
-scaled-dot-product over the whole sequence instead of the paged KV path.  A token the
+weights, the oracle's restatements of the reference layers (oracle/layers_oracle.py)
+and attention as a causal fp32 scaled-dot-product over the whole sequence: no kernel of
+libkvpath.so is involved, only torch GEMMs.  A token the
 engine generated greedily is accepted when its reference logit is within `tol` of the
 reference maximum at that position (near-ties may legitimately flip under bf16).
 """
@@ -12,7 +13,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from kavor_amd.engine.qwen3 import add_rms_norm, apply_rope, rms_norm
+from oracle.layers_oracle import add_rms_norm, apply_rope, rms_norm, silu_and_mul
 
 
 @torch.inference_mode()
@@ -44,7 +45,7 @@ def reference_logits(model, token_ids: list[int]) -> torch.Tensor:
         o = o.transpose(0, 1).to(torch.bfloat16).reshape(T, -1)
         h = F.linear(o, a.o_proj)
         x, residual = add_rms_norm(h, residual, layer.post_attention_layernorm.weight, spec.rms_norm_eps)
-        h = layer.mlp(x)
+        h = F.linear(silu_and_mul(F.linear(x, layer.mlp.gate_up_proj)), layer.mlp.down_proj)
     h, _ = add_rms_norm(h, residual, model.norm.weight, spec.rms_norm_eps)
     return F.linear(h, model.lm_head).float()
 
