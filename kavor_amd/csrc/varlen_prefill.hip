@@ -18,13 +18,12 @@
 //   O^T += V^T P^T (M = 128 dims, N = 32 rows, K-dim = 64 keys), reading the V^T operand
 //   with the gfx950 LDS transpose load (ds_read_b64_tr_b16).  With the transposed
 //   products every lane holds whole columns of its own query row (row = lane % 32), so
-//   the online-softmax max / sum / rescale need only one cross-lane exchange (lane^32)
-//   and P feeds the second MFMA straight from registers.
+//   the online-softmax max / sum / rescale need only one exchange between the wave halves
+//   (v_permlane32_swap, no LDS) and P feeds the second MFMA straight from registers.  The
+//   softmax scale is folded into the exponent (exp2(fma(s, scale*log2 e, -m))).
 //   Q stays in registers for the whole key loop (8 x 16 bytes per lane).
-//   The 1-D grid is remapped so that consecutive work items (the query tiles of one
-//   sequence and kv head, and neighbouring sequences that share prefix blocks) run on
-//   the same XCD and share its L2; within a (sequence, kv head) the longest (last)
-//   query tiles are dispatched first.
+//   The 1-D grid runs the longest (last) query tile of every sequence and kv head
+//   first, then the second-to-last ones, and so on.
 #include <math.h>
 
 #include "common.h"
@@ -40,7 +39,6 @@ constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows (token x head) p
 constexpr int kKeyTile = 64;
 constexpr int kKStride = kPrefillHeadDim + 8;  // LDS row pitch of the K tile (bf16)
 constexpr int kVStride = kPrefillHeadDim + 8;  // LDS row pitch of the V tile (bf16)
-constexpr int kNumXcd = 8;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -77,6 +75,17 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* lds_ptr) {
   return __builtin_bit_cast(uint2, v);
 }
 
+// Max / sum of x over lanes l and l ^ 32 (v_permlane32_swap_b32 exchanges the wave halves:
+// the first result holds lanes 0-31 in both halves, the second lanes 32-63).
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -91,13 +100,18 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   constexpr int D = kPrefillHeadDim;
   constexpr int TOK = kPrefillRows / G;  // query tokens per tile
 
-  // XCD-aware work index: hardware places workgroup id i on XCD i % 8.
-  const int per_xcd = (p.total_work + kNumXcd - 1) / kNumXcd;
-  const int work = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+  // Work order: tile slot major (slot 0 = the last, longest query tile of every sequence,
+  // then the second-to-last, ...), then sequence, then kv head.  Long tiles start first
+  // and the short ones fill in behind them; consecutive workgroup ids (which the
+  // hardware deals round-robin to the 8 XCDs) carry work of similar size.  Measured on
+  // the prefix-cached 32-sequence workload: 0.82 ms with (sequence, kv head, tile)
+  // order dealt to XCDs in contiguous chunks, 0.58 ms with this order.
+  const int work = blockIdx.x;
   if (work >= p.total_work) return;
-  const int tile_slot = work % p.num_tiles;
-  const int kvh = (work / p.num_tiles) % p.num_kv_heads;
-  const int s = work / (p.num_tiles * p.num_kv_heads);
+  const int nseq = p.total_work / (p.num_tiles * p.num_kv_heads);
+  const int tile_slot = work / (nseq * p.num_kv_heads);
+  const int kvh = work % p.num_kv_heads;
+  const int s = (work / p.num_kv_heads) % nseq;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -123,14 +137,21 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   if (tid == 0) s_bad = 0;  // sticky for the workgroup: one sequence, one block table
   __syncthreads();
 
-  // Thread t stages 16-byte chunk (t % 16) of keys t/16 + (threads/16)*u of a 64-key tile.
+  // The first 64 block-table entries of the sequence, one per lane, read with readlane:
+  // a tile's block id then costs no memory round trip on the way to its K/V loads.
+  int bt_lane = -1;
+  if (PAGED && lane < p.max_blocks) bt_lane = p.block_tables[s * p.bt_stride + lane];
+
+  // Thread t stages 16-byte chunk (t % 16) of keys t/16 + (threads/16)*u of a 64-key tile;
+  // keys past the context are staged as zeros.
   const int chunk = tid & 15;
   auto load_tile = [&](int kv0, uint4 (&kc)[kStageIters], uint4 (&vc)[kStageIters]) {
     int64_t kbase = 0, vbase = 0;
     bool blk_ok = true;
     if (PAGED) {
       const int lblk = kv0 / p.block_size;
-      int blk = (lblk < p.max_blocks) ? p.block_tables[s * p.bt_stride + lblk] : -1;
+      int blk = lblk < 64 ? __builtin_amdgcn_readlane(bt_lane, lblk)
+                          : (lblk < p.max_blocks ? p.block_tables[s * p.bt_stride + lblk] : -1);
       if (blk < 0 || blk >= p.num_cache_blocks) {
         blk_ok = false;
         blk = 0;
@@ -232,15 +253,12 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       // tile max exceeds it by more than 2^8, so O is rescaled rarely; P <= 2^8 stays
       // exact enough in bf16 (the relative precision does not depend on magnitude).
       const bool interior = kv0 + kKeyTile - 1 <= min(klen - 1, wave_min_limit);
-      float mx = kMaxFloor;
+      float mx = kMaxFloor;  // raw (unscaled) scores; scale > 0 keeps their order
       if (interior) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            sacc[mb][j] *= p.scale_log2;
-            mx = fmaxf(mx, sacc[mb][j]);
-          }
+          for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sacc[mb][j]);
       } else {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
@@ -248,11 +266,11 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
           for (int j = 0; j < 16; ++j) {
             const int key = kv0 + 32 * mb + 8 * (j >> 2) + 4 * hf + (j & 3);
             const bool ok = key < klen && key <= row_limit;
-            sacc[mb][j] = ok ? sacc[mb][j] * p.scale_log2 : -INFINITY;
+            sacc[mb][j] = ok ? sacc[mb][j] : -INFINITY;
             mx = fmaxf(mx, sacc[mb][j]);
           }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = half_swap_max(mx) * p.scale_log2;
       const bool grow = mx > m_run + 8.f;
       if (__any(grow)) {
         const float m_new = grow ? mx : m_run;
@@ -270,12 +288,12 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
-          const float p0 = fast_exp2(sacc[mb][j] - m_run);
-          const float p1 = fast_exp2(sacc[mb][j + 1] - m_run);
+          const float p0 = fast_exp2(fmaf(sacc[mb][j], p.scale_log2, -m_run));
+          const float p1 = fast_exp2(fmaf(sacc[mb][j + 1], p.scale_log2, -m_run));
           rsum += p0 + p1;
           pk[mb][j >> 1] = pack_bf16x2(p0, p1);
         }
-      rsum += __shfl_xor(rsum, 32);
+      rsum = half_swap_sum(rsum);
       l_run += rsum;
 
       // ---- O^T += V^T P^T : K-dim step kk covers keys 16kk..16kk+15.  This lane's P
@@ -413,8 +431,7 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
   p.o_tok_stride = out_tok_stride;
   p.o_head_stride = out_head_stride;
 
-  const int per_xcd = static_cast<int>((total + kNumXcd - 1) / kNumXcd);
-  const dim3 grid(per_xcd * kNumXcd);
+  const dim3 grid(static_cast<unsigned>(total));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool c = causal != 0;
   switch (G) {
