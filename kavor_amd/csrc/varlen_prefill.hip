@@ -38,7 +38,7 @@ constexpr int kStageIters = 64 * 16 / kPrefillThreads;
 constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows (token x head) per workgroup
 constexpr int kKeyTile = 64;
 constexpr int kKStride = kPrefillHeadDim + 8;  // LDS row pitch of the K tile (bf16)
-constexpr int kVStride = kPrefillHeadDim + 8;  // LDS row pitch of the V tile (bf16)
+constexpr int kVStride = kPrefillHeadDim + 32;  // LDS row pitch of the V tile (bf16): 80 dwords keeps the transposed reads conflict-free
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
