@@ -134,6 +134,87 @@ def bench_append(dev, steps, warmup):
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
 
 
+LAYER_TOKENS = 16384  # one full prefill step of the engine (max_num_batched_tokens)
+
+
+def layer_inputs(dev, T=LAYER_TOKENS):
+    """Qwen3-0.6B layer tensors for T tokens: fused qkv rows, an interleaved page pool
+    with one 256-token block per 256 tokens (in shuffled order), residual stream rows,
+    gate|up rows, and a [256, 151936] logits block."""
+    from kavor_amd.engine.qwen3 import rope_cache
+
+    hq, hkv, H, I = 16, 8, 1024, 3072
+    dg = torch.Generator(device=dev).manual_seed(0)
+    g = torch.Generator().manual_seed(0)
+    nb = T // BS
+    page = 2 * BS * hkv * D * 2
+    pool = torch.zeros(nb, page, dtype=torch.uint8, device=dev)
+    flat = pool.view(torch.bfloat16)
+    shape, strides = (nb, BS, hkv, D), (page // 2, hkv * D, D, 1)
+    kc = flat.as_strided(shape, strides, 0)
+    vc = flat.as_strided(shape, strides, BS * hkv * D)
+    blocks = torch.randperm(nb, generator=g)
+    slots = (blocks.repeat_interleave(BS) * BS + torch.arange(T) % BS).to(torch.int32)
+    return dict(
+        qkv=torch.randn(T, (hq + 2 * hkv) * D, generator=dg, device=dev, dtype=torch.bfloat16),
+        pos=(torch.arange(T) % 4096).to(torch.int32).to(dev),
+        table=rope_cache(D, 40960, 1e6, dev), qw=torch.ones(D, device=dev, dtype=torch.bfloat16),
+        kc=kc, vc=vc, slots=slots.to(dev),
+        x=torch.randn(T, H, generator=dg, device=dev, dtype=torch.bfloat16),
+        res=torch.randn(T, H, generator=dg, device=dev, dtype=torch.bfloat16),
+        w=torch.ones(H, device=dev, dtype=torch.bfloat16),
+        gu=torch.randn(T, 2 * I, generator=dg, device=dev, dtype=torch.bfloat16),
+        logits=torch.randn(256, 151936, generator=dg, device=dev, dtype=torch.bfloat16),
+        hq=hq, hkv=hkv, H=H, I=I, T=T)
+
+
+def layer_algo_bytes(inp) -> dict:
+    """Algorithmic HBM bytes per launch of each fused layer kernel."""
+    T, hq, hkv, H, I = inp["T"], inp["hq"], inp["hkv"], inp["H"], inp["I"]
+    return {
+        # read the qkv row, write q, write k and v into the pages, read position and slot
+        "qk_norm_rope_append": T * ((hq + 2 * hkv) * D * 2 + hq * D * 2 + 2 * hkv * D * 2 + 8),
+        # read x and the residual, write the residual and the output
+        "add_rmsnorm": T * H * 2 * 4,
+        # read gate|up, write the product
+        "silu_mul": T * I * 2 * 3,
+        # read the logits rows, write one int64 per row
+        "argmax": 256 * 151936 * 2 + 256 * 8,
+    }
+
+
+def layer_launchers(inp):
+    from kavor_amd.layers import fused
+
+    q_out = torch.empty(inp["T"], inp["hq"], D, device=inp["qkv"].device, dtype=torch.bfloat16)
+    out = torch.empty_like(inp["x"])
+    s_out = torch.empty(inp["T"], inp["I"], device=inp["x"].device, dtype=torch.bfloat16)
+    tok = torch.empty(256, dtype=torch.int64, device=inp["x"].device)
+    return {
+        "qk_norm_rope_append": lambda: fused.qk_norm_rope_append(
+            inp["qkv"], inp["pos"], inp["table"], inp["qw"], inp["qw"], 1e-6, inp["hq"], inp["hkv"],
+            inp["kc"], inp["vc"], inp["slots"], q_out=q_out),
+        "add_rmsnorm": lambda: fused.add_rms_norm(inp["x"], inp["res"], inp["w"], 1e-6, out=out),
+        "silu_mul": lambda: fused.silu_and_mul(inp["gu"], out=s_out),
+        "argmax": lambda: fused.greedy_argmax(inp["logits"], out=tok),
+    }
+
+
+def bench_layers(dev, steps, warmup):
+    """The fused kernels around the path at one full engine prefill step (16384 tokens of
+    Qwen3-0.6B) and the greedy argmax over a 256 x 151936 logits block."""
+    inp = layer_inputs(dev)
+    algo = layer_algo_bytes(inp)
+    res = {}
+    for name, fn in layer_launchers(inp).items():
+        ms = time_launches(fn, steps, warmup)
+        res[name] = dict(us=round(ms * 1e3, 2), gbs=round(algo[name] / ms / 1e6, 1),
+                         frac=round(algo[name] / ms / 1e6 / HBM_PEAK_GBS, 4), bytes=algo[name])
+    res["workload"] = (f"{inp['T']} tokens, Qwen3-0.6B layer (16q/8kv heads, hidden 1024, intermediate "
+                       "3072); argmax over [256, 151936] bf16 logits")
+    return res
+
+
 def bench_prefill(dev, steps, warmup):
     from kavor_amd.layers.attention import varlen_prefill
     from oracle.kvpath_oracle import prefill_flops
@@ -214,24 +295,52 @@ def load_traffic(name: str):
         return None
 
 
-def profile_run(dev) -> int:
-    """Fixed launch sequence for rocprofv3 counter runs: 3 plain 1 GiB copies (the
-    calibration of the byte counters), then (after warm-up launches) 40 decode steps of
-    the Qwen3-0.6B workload, 48 KV appends (two graph replays), 6 prefix-cached prefills
-    and 8 decode steps of the Qwen3-8B workload."""
-    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+def extra_counts(steps: int, warmup: int) -> dict:
+    """Timed and warm-up launches of each extra workload: enough work after warm-up that
+    the clocks have settled (a 0.5 ms prefill timed 10 times right after 2 warm-ups reads
+    7-15% slow on this part)."""
+    return dict(append=(steps, warmup), prefill=(max(20, steps // 3), max(10, warmup // 3)),
+                layers=(max(20, steps // 2), max(10, warmup // 3)),
+                decode_8b=(max(20, steps // 4), max(5, warmup // 6)))
+
+
+def run_extras(dev, steps: int, warmup: int) -> dict:
+    n = extra_counts(steps, warmup)
+    extras = {}
+    a = bench_append(dev, *n["append"])
+    extras["kv_append"] = dict(gbs=round(a["gbs"], 1), frac=round(a["gbs"] / HBM_PEAK_GBS, 4),
+                               us=round(a["ms"] * 1e3, 3), bytes=a["bytes"],
+                               workload="4096 tok x 8 kv heads x 128 bf16, 3968 valid + 128 pad slots, "
+                                        "cache [512,256,8,128], 24 rotating input sets, graph-replayed")
+    torch.cuda.empty_cache()
+    p = bench_prefill(dev, *n["prefill"])
+    extras["varlen_prefill"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                    ms=round(p["ms"], 4), flops=p["flops"],
+                                    workload="32 seqs, new 100-1024, prefix 0-4096 shared by groups of 4, 16q/8kv")
+    torch.cuda.empty_cache()
+    extras["layer_kernels"] = bench_layers(dev, *n["layers"])
+    torch.cuda.empty_cache()
+    _, c = bench_decode(dev, *n["decode_8b"], "qwen3_8b")
+    extras["paged_decode_qwen3_8b"] = dict(gbs=round(c["gbs"], 1), frac=round(c["gbs"] / HBM_PEAK_GBS, 4),
+                                           ms=round(c["ms"], 4), bytes=c["bytes"],
+                                           workload="B=128, 32q/8kv, ctx U[1024,32768], pool 20000 blocks")
+    torch.cuda.empty_cache()
+    return extras
+
+
+def profile_run(dev, steps: int, warmup: int) -> int:
+    """The default bench's kernel launches, for rocprofv3: three plain 1 GiB copies first
+    (the calibration of the byte counters), then the headline decode and every extra
+    workload with the same launch counts as the timed run (no CPU baseline, no engine)."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)  # calibration copies
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    bench_decode(dev, 40, 3, "qwen3_0.6b")
+    bench_decode(dev, steps, warmup, "qwen3_0.6b")
     torch.cuda.empty_cache()
-    bench_append(dev, 48, 3)
-    torch.cuda.empty_cache()
-    bench_prefill(dev, 6, 1)
-    torch.cuda.empty_cache()
-    bench_decode(dev, 8, 1, "qwen3_8b")
+    run_extras(dev, steps, warmup)
     torch.cuda.synchronize()
     print("profile run done", flush=True)
     return 0
@@ -251,6 +360,10 @@ PROFILE_KERNELS = [
     ("paged_decode_qwen3_8b", "void kvp::paged_decode_kernel<4,", "decode_8b"),
     ("kv_append_4096tok", "void kvp::kv_append_kernel<128", "append"),
     ("varlen_prefill_prefix_32seq", "void kvp::varlen_prefill_kernel<2, true, true>", "prefill"),
+    ("qk_norm_rope_append_16384tok", "kvp::(anonymous namespace)::qk_norm_rope_append_kernel", "qk_norm_rope_append"),
+    ("add_rmsnorm_16384x1024", "void kvp::(anonymous namespace)::rmsnorm_kernel<64, 2>", "add_rmsnorm"),
+    ("silu_mul_16384x3072", "kvp::(anonymous namespace)::silu_mul_kernel", "silu_mul"),
+    ("argmax_256x151936", "kvp::(anonymous namespace)::argmax_kernel", "argmax"),
 ]
 
 
@@ -287,6 +400,7 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         "append": 32522240,
         "prefill": 352688504832,
     }
+    algo.update(layer_algo_bytes(dict(T=LAYER_TOKENS, hq=16, hkv=8, H=1024, I=3072)))
     out_dir = ROOT / "profiles"
     out_dir.mkdir(exist_ok=True)
     merge_name = "kvp::decode_merge_kernel(kvp::DecodeParams)"
@@ -295,7 +409,8 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         if not names:
             continue
         name = names[0]
-        d_us = [x / 1e3 for x in dur[name]]
+        all_us = [x / 1e3 for x in dur[name]]
+        d_us = all_us[len(all_us) // 3:]  # the first third covers the warm-up launches
         fetch = [x * f_scale * 1024 for x in counters["FETCH_SIZE"].get(name, [])]
         write = [x * w_scale * 1024 for x in counters["WRITE_SIZE"].get(name, [])]
         avg_us = statistics.mean(d_us)
@@ -304,8 +419,9 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
                  "Commands (from the repository root on the GPU host, `R=$PWD`):", "", "```"]
         lines += PROFILE_CMDS + ["```", ""]
         med_us = statistics.median(d_us)
-        lines += [f"- dispatches: {len(d_us)} (warm-up launches included); duration avg {avg_us:.2f} us, "
-                  f"median {med_us:.2f} us, min {min(d_us):.2f}, max {max(d_us):.2f}"]
+        lines += [f"- dispatches: {len(all_us)}; over the last {len(d_us)} (after the warm-up launches) "
+                  f"duration avg {avg_us:.2f} us, median {med_us:.2f} us, min {min(d_us):.2f}, "
+                  f"max {max(d_us):.2f}"]
         if key == "prefill":
             lines += [f"- algorithmic work: {algo[key]} flop (unmasked query-key pairs x 4 x Hq x D) "
                       f"-> {algo[key] / med_us / 1e6:.1f} TFLOP/s at the median duration "
@@ -320,6 +436,7 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
                   + (f" = {traffic / algo[key]:.4f} x algorithmic" if key != "prefill" else "")]
         if key.startswith("decode") and merge_name in dur:
             m_us = [x / 1e3 for x in dur[merge_name]]
+            m_us = m_us[len(m_us) // 3:]
             lines += [f"- the decode's split-combining `{merge_name}` (all decode workloads): "
                       f"median {statistics.median(m_us):.2f} us over {len(m_us)} dispatches"]
         (out_dir / f"{fname}.md").write_text("\n".join(lines) + "\n")
@@ -328,6 +445,48 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
                 {"kernel": name, "traffic_bytes": int(round(traffic)), "fetch_scale": f_scale,
                  "write_scale": w_scale, "median_duration_us": med_us}, indent=1) + "\n")
         print(f"{fname}: median {med_us:.2f} us, traffic {traffic:.0f} B", flush=True)
+    return 0
+
+
+E2E_PROFILE_CMDS = [
+    "cd /tmp && export TMPDIR=/tmp",
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/e2e_trace -o run -- python $R/bench.py --e2e-only",
+    "python $R/bench.py --summarize-e2e $R/gpurun_out/e2e_trace",
+]
+
+
+def summarize_e2e(trace_dir: str) -> int:
+    """profiles/e2e_qwen3_0.6b.md: where the end-to-end generation spends GPU time, from
+    the --stats output of rocprofv3 over `bench.py --e2e-only`."""
+    import csv
+
+    with open(Path(trace_dir) / "run_kernel_stats.csv") as f:
+        rows = list(csv.DictReader(f))
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+
+    def group(name):
+        if name.startswith("Cijk") or name.startswith("Custom_Cijk"):
+            return "hipBLASLt GEMMs (projections, MLP, LM head)"
+        if "kvp::" in name:
+            return name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+        return "other (torch: embedding, copies, fills)"
+
+    by = {}
+    for r in rows:
+        g = group(r["Name"])
+        t, c = by.get(g, (0.0, 0))
+        by[g] = (t + float(r["TotalDurationNs"]), c + int(r["Calls"]))
+    lines = ["# e2e_qwen3_0.6b: GPU time of the end-to-end generation, by kernel", "",
+             "Commands (from the repository root on the GPU host, `R=$PWD`):", "", "```"]
+    lines += E2E_PROFILE_CMDS + ["```", "",
+                                 f"Total kernel time {total / 1e9:.3f} s (profiler overhead included; the "
+                                 "untraced run's wall time is in bench.py's e2e_qwen3_0.6b field).", "",
+                                 "| kernel | calls | total s | share | avg us |", "|---|---|---|---|---|"]
+    for g, (t, c) in sorted(by.items(), key=lambda x: -x[1][0]):
+        lines.append(f"| `{g}` | {c} | {t / 1e9:.3f} | {100 * t / total:.1f}% | {t / c / 1e3:.2f} |")
+    out = ROOT / "profiles" / "e2e_qwen3_0.6b.md"
+    out.write_text("\n".join(lines) + "\n")
+    print(f"wrote {out}", flush=True)
     return 0
 
 
@@ -411,8 +570,8 @@ def bench_e2e(num_seqs: int = 256):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-extras", action="store_true", help="headline decode workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen3-0.6B generation")
@@ -423,11 +582,16 @@ def main() -> int:
                          "three rocprofv3 runs of --profile: --kernel-trace --stats, --pmc "
                          "FETCH_SIZE, --pmc WRITE_SIZE")
     ap.add_argument("--profile", action="store_true",
-                    help="launch each kernel a few times (no timing) under rocprofv3; starts with a "
-                         "plain 1 GiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE")
+                    help="the default run's kernel launches without the CPU baseline and the engine, "
+                         "for rocprofv3; starts with plain 1 GiB device copies used to calibrate "
+                         "FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--summarize-e2e", metavar="TRACE_DIR",
+                    help="write profiles/e2e_qwen3_0.6b.md from rocprofv3 --stats over --e2e-only")
     args = ap.parse_args()
     if args.summarize:
         return summarize_profiles(*args.summarize)
+    if args.summarize_e2e:
+        return summarize_e2e(args.summarize_e2e)
     if args.gpus != 1:
         print(f"bench.py measures one GPU's paged KV-cache kernels; --gpus {args.gpus} is not "
               "supported (the path shards by kv head with no exchange inside attention).", file=sys.stderr)
@@ -440,7 +604,7 @@ def main() -> int:
 
     lib()
     if args.profile:
-        return profile_run(dev)
+        return profile_run(dev, args.steps, args.warmup)
     if args.e2e_only:
         print(json.dumps({"e2e_qwen3_0.6b": bench_e2e(args.e2e_seqs)}), flush=True)
         return 0
@@ -448,20 +612,7 @@ def main() -> int:
     inp, dec = bench_decode(dev, args.steps, args.warmup, "qwen3_0.6b")
     extras = {}
     if not args.no_extras:
-        a = bench_append(dev, args.steps, args.warmup)
-        extras["kv_append"] = dict(gbs=round(a["gbs"], 1), frac=round(a["gbs"] / HBM_PEAK_GBS, 4),
-                                   us=round(a["ms"] * 1e3, 3), bytes=a["bytes"],
-                                   workload="4096 tok x 8 kv heads x 128 bf16, 3968 valid + 128 pad slots, "
-                                            "cache [512,256,8,128], 24 rotating input sets, graph-replayed")
-        p = bench_prefill(dev, max(5, args.steps // 5), 2)
-        extras["varlen_prefill"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                        ms=round(p["ms"], 4), flops=p["flops"],
-                                        workload="32 seqs, new 100-1024, prefix 0-4096 shared by groups of 4, 16q/8kv")
-        _, c = bench_decode(dev, max(10, args.steps // 2), 3, "qwen3_8b")
-        extras["paged_decode_qwen3_8b"] = dict(gbs=round(c["gbs"], 1), frac=round(c["gbs"] / HBM_PEAK_GBS, 4),
-                                               ms=round(c["ms"], 4), bytes=c["bytes"],
-                                               workload="B=128, 32q/8kv, ctx U[1024,32768], pool 20000 blocks")
-        torch.cuda.empty_cache()
+        extras.update(run_extras(dev, args.steps, args.warmup))
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(inp)
     if not args.no_e2e:
         del inp
