@@ -174,12 +174,21 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     if (!blk_ok) bad = true;
     kbase += static_cast<int64_t>(kvh) * p.k_head_stride + 8 * chunk;
     vbase += static_cast<int64_t>(kvh) * p.v_head_stride + 8 * chunk;
+    if (kv0 + kKeyTile <= klen && blk_ok) {  // whole tile inside the context (uniform)
 #pragma unroll
-    for (int u = 0; u < kStageIters; ++u) {
-      const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
-      const bool ok = kv0 + key < klen && blk_ok;
-      kc[u] = ok ? *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride) : make_uint4(0, 0, 0, 0);
-      vc[u] = ok ? *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride) : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < kStageIters; ++u) {
+        const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
+        kc[u] = *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride);
+        vc[u] = *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kStageIters; ++u) {
+        const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
+        const bool ok = kv0 + key < klen && blk_ok;
+        kc[u] = ok ? *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride) : make_uint4(0, 0, 0, 0);
+        vc[u] = ok ? *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride) : make_uint4(0, 0, 0, 0);
+      }
     }
   };
 
@@ -245,6 +254,9 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
 
       // ---- S^T = K Q^T : two 32-key blocks, lane holds keys of its own query row
       f32x16_t sacc[2];
+      // MFMA blocks run at wave priority 1 and the softmax at 0: of the two waves a SIMD
+      // holds, the one with matrix work issues first and the other's VALU fills in.
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
@@ -256,6 +268,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         }
       }
 
+      __builtin_amdgcn_s_setprio(0);
       // ---- online softmax over this tile (base 2).  Interior tiles (every key visible
       // to every row of the wave) skip the mask.  The running max only moves when a row's
       // tile max exceeds it by more than 2^8, so O is rescaled rarely; P <= 2^8 stays
@@ -306,6 +319,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
 
       // ---- O^T += V^T P^T : K-dim step kk covers keys 16kk..16kk+15.  This lane's P
       // registers for that step hold key offsets {4hf+0..3, 8+4hf+0..3}.
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kk = 0; kk < kKeyTile / 16; ++kk) {
         const int mbs = kk >> 1;
@@ -320,6 +334,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     if (bad) s_bad = 1;
     __syncthreads();
