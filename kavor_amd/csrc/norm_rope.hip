@@ -142,74 +142,93 @@ struct QkParams {
   int num_tokens, hq, hkv, block_size;
 };
 
-// One 16-lane row handles one head of one token: rows [0, hq) are q heads, [hq, hq+hkv)
-// k heads, [hq+hkv, hq+2hkv) v heads.  Lane j of the row holds elements 8j..8j+7; the RoPE
-// partner of element i (< 64) is i + 64, which lives in lane j ^ 8 (DPP row_ror:8).
-__global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(QkParams p) {
-  const int lane = threadIdx.x & 15;
-  const int heads = p.hq + 2 * p.hkv;
-  const int64_t grow = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4);
-  if (grow >= static_cast<int64_t>(p.num_tokens) * heads) return;  // uniform across the row
-  const int t = static_cast<int>(grow / heads);
-  const int r = static_cast<int>(grow - static_cast<int64_t>(t) * heads);
-  const uint4 raw = load16(p.qkv + t * p.qkv_stride + r * kRopeDim + 8 * lane);
+// One wave per token; its four 16-lane rows take heads r, r+4, r+8, ... (r = lane / 16):
+// heads [0, hq) are q heads, [hq, hq+hkv) k heads, [hq+hkv, hq+2hkv) v heads.  Lane j of a
+// row holds elements 8j..8j+7 of its head, so its cos/sin values and norm weights are the
+// same for every head: they are loaded once per token, and the wave issues the loads of
+// up to kRopeBatch heads per row before computing any of them.  The RoPE partner of
+// element i (< 64) is i + 64, which lives in lane j ^ 8 (DPP row_ror:8).
+constexpr int kRopeBatch = 8;  // heads per row in flight (32 heads per wave)
 
-  const int slot = p.slot_mapping ? p.slot_mapping[t] : -1;
-  const bool store_kv = slot >= 0 && slot < p.num_cache_slots;
-  int64_t cache_off = 0;
-  if (store_kv) {
-    const int blk = slot / p.block_size, off = slot - blk * p.block_size;
-    cache_off = blk * p.blk_stride + off * p.slot_stride + 8 * lane;
-  }
-  if (r >= p.hq + p.hkv) {  // v head: bit copy into the cache
-    if (store_kv) store16(p.v_cache + cache_off + (r - p.hq - p.hkv) * p.head_stride, raw);
-    return;
-  }
-  const bool is_q = r < p.hq;
-  if (!is_q && !store_kv) return;  // k head of a padding token (uniform across the row)
-  float x[8], w[8];
-  unpack8(raw, x);
-  unpack8(load16((is_q ? p.q_weight : p.k_weight) + 8 * lane), w);
+__device__ __forceinline__ void norm_rope_head(float (&x)[8], const float (&w)[8], const float (&c)[8],
+                                               const float (&sn)[8], bool first_half, bool pos_ok,
+                                               float eps) {
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
   ss = row16_sum(ss);
-  const float rstd = rsqrtf(ss * (1.0f / kRopeDim) + p.eps);
+  const float rstd = rsqrtf(ss * (1.0f / kRopeDim) + eps);
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = round_bf16(round_bf16(x[e] * rstd) * w[e]);
-
-  // partner half: the same 8 elements of lane ^ 8
-  uint4 mine = pack8(x), other;
+  const uint4 mine = pack8(x);
+  uint4 other;
   other.x = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.x), 0x128, 0xf, 0xf, false));
   other.y = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.y), 0x128, 0xf, 0xf, false));
   other.z = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.z), 0x128, 0xf, 0xf, false));
   other.w = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.w), 0x128, 0xf, 0xf, false));
   float y[8];
   unpack8(other, y);
-
-  int pos = p.positions[t];
-  const bool pos_ok = pos >= 0 && pos < p.max_position;
-  pos = pos_ok ? pos : 0;
-  const int fi = 8 * (lane & 7);  // frequency index of this lane's first element
-  const float* cs = p.cos_sin + static_cast<int64_t>(pos) * kRopeDim;
-  float c[8], s[8];
-  *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(cs + fi);
-  *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(cs + fi + 4);
-  *reinterpret_cast<float4*>(s) = *reinterpret_cast<const float4*>(cs + kRopeDim / 2 + fi);
-  *reinterpret_cast<float4*>(s + 4) = *reinterpret_cast<const float4*>(cs + kRopeDim / 2 + fi + 4);
-  const bool first_half = lane < 8;
-  float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     // first half: x1*cos - x2*sin; second half: x2*cos + x1*sin
-    o[e] = first_half ? x[e] * c[e] - y[e] * s[e] : x[e] * c[e] + y[e] * s[e];
-    if (!pos_ok) o[e] = __builtin_nanf("");
+    const float o = first_half ? x[e] * c[e] - y[e] * sn[e] : x[e] * c[e] + y[e] * sn[e];
+    x[e] = pos_ok ? o : __builtin_nanf("");
   }
-  const uint4 packed = pack8(o);
-  if (is_q) {
-    store16(p.q_out + t * p.q_out_stride + r * kRopeDim + 8 * lane, packed);
-  } else if (store_kv) {
-    store16(p.k_cache + cache_off + (r - p.hq) * p.head_stride, packed);
+}
+
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(QkParams p) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane >> 4, j = lane & 15;
+  const int t = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (t >= p.num_tokens) return;  // uniform across the wave
+  const int heads = p.hq + 2 * p.hkv;
+  const uint16_t* row = p.qkv + t * p.qkv_stride + 8 * j;
+
+  const int slot = p.slot_mapping ? p.slot_mapping[t] : -1;
+  const bool store_kv = slot >= 0 && slot < p.num_cache_slots;
+  int64_t cache_off = 0;
+  if (store_kv) {
+    const int blk = slot / p.block_size, off = slot - blk * p.block_size;
+    cache_off = blk * p.blk_stride + off * p.slot_stride + 8 * j;
+  }
+  int pos = p.positions[t];
+  const bool pos_ok = pos >= 0 && pos < p.max_position;
+  pos = pos_ok ? pos : 0;
+  const int fi = 8 * (j & 7);  // frequency index of this lane's first element
+  const float* cs = p.cos_sin + static_cast<int64_t>(pos) * kRopeDim;
+  float c[8], sn[8], wq[8], wk[8];
+  *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(cs + fi);
+  *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(cs + fi + 4);
+  *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(cs + kRopeDim / 2 + fi);
+  *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(cs + kRopeDim / 2 + fi + 4);
+  unpack8(load16(p.q_weight + 8 * j), wq);
+  unpack8(load16(p.k_weight + 8 * j), wk);
+  const bool first_half = j < 8;
+
+  for (int h0 = 0; h0 < heads; h0 += 4 * kRopeBatch) {
+    uint4 raw[kRopeBatch];
+#pragma unroll
+    for (int u = 0; u < kRopeBatch; ++u) {
+      const int h = min(h0 + 4 * u + r, heads - 1);  // clamped: rows past the last head idle below
+      raw[u] = load16(row + h * kRopeDim);
+    }
+#pragma unroll
+    for (int u = 0; u < kRopeBatch; ++u) {
+      const int h = h0 + 4 * u + r;  // uniform across the 16-lane row
+      if (h >= heads) continue;
+      if (h >= p.hq + p.hkv) {  // v head: bit copy into the cache
+        if (store_kv) store16(p.v_cache + cache_off + (h - p.hq - p.hkv) * p.head_stride, raw[u]);
+        continue;
+      }
+      const bool is_q = h < p.hq;
+      if (!is_q && !store_kv) continue;  // k head of a padding token
+      float x[8];
+      unpack8(raw[u], x);
+      norm_rope_head(x, is_q ? wq : wk, c, sn, first_half, pos_ok, p.eps);
+      const uint4 packed = pack8(x);
+      if (is_q) store16(p.q_out + t * p.q_out_stride + h * kRopeDim + 8 * j, packed);
+      else store16(p.k_cache + cache_off + (h - p.hq) * p.head_stride, packed);
+    }
   }
 }
 
@@ -243,6 +262,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(SiluParams p) {
 // ------------------------------------------------------------------ argmax
 
 constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxBatch = 8;
 
 struct ArgmaxParams {
   const uint16_t* logits;
@@ -264,12 +284,23 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(ArgmaxParams p) 
   float best = -__builtin_inff();
   int bi = 0x7fffffff;
   const int nvec = p.vocab >> 3;
-  for (int c = threadIdx.x; c < nvec; c += kArgmaxThreads) {
-    float f[8];
-    unpack8(load16_nt(row + 8 * c), f);
+  // kArgmaxBatch 16-byte loads per thread in flight before any is scanned; indices past
+  // the row are clamped onto its last chunk and skipped.
+  for (int c0 = threadIdx.x; c0 < nvec; c0 += kArgmaxThreads * kArgmaxBatch) {
+    uint4 w[kArgmaxBatch];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (beats(f[e], 8 * c + e, best, bi)) { best = f[e]; bi = 8 * c + e; }
+    for (int u = 0; u < kArgmaxBatch; ++u)
+      w[u] = load16_nt(row + 8 * min(c0 + u * kArgmaxThreads, nvec - 1));
+#pragma unroll
+    for (int u = 0; u < kArgmaxBatch; ++u) {
+      const int c = c0 + u * kArgmaxThreads;
+      if (c >= nvec) break;
+      float f[8];
+      unpack8(w[u], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (beats(f[e], 8 * c + e, best, bi)) { best = f[e]; bi = 8 * c + e; }
+    }
   }
   const int tail = p.vocab - 8 * nvec;
   if (static_cast<int>(threadIdx.x) < tail) {
@@ -363,10 +394,8 @@ extern "C" int kvp_qk_norm_rope_append_bf16(
   if (qkv_tok_stride < static_cast<int64_t>(num_q_heads + 2 * num_kv_heads) * head_dim)
     return fail(KVP_EINVAL, "qkv row stride %lld is shorter than (hq + 2 hkv) * head_dim",
                 (long long)qkv_tok_stride);
-  const int64_t heads = num_q_heads + 2 * num_kv_heads;
-  const int64_t rows = static_cast<int64_t>(num_tokens) * heads;
-  if (rows == 0) return KVP_OK;
-  const int64_t grid = (rows + kThreads / 16 - 1) / (kThreads / 16);
+  if (num_tokens == 0) return KVP_OK;
+  const int64_t grid = (static_cast<int64_t>(num_tokens) + kThreads / 64 - 1) / (kThreads / 64);
   if (grid > INT32_MAX) return fail(KVP_EINVAL, "too many tokens");
   QkParams p{static_cast<const uint16_t*>(qkv), qkv_tok_stride, positions, cos_sin, max_position,
              static_cast<const uint16_t*>(q_norm_weight), static_cast<const uint16_t*>(k_norm_weight),
