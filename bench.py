@@ -131,7 +131,21 @@ def bench_append(dev, steps, warmup):
     replays = max(2, (steps if steps < 16 else max(steps, 48)) // len(sets))
     ms = time_launches(graph.replay, replays, max(1, warmup // len(sets))) / len(sets)
     nbytes = append_bytes(sets[0][2].cpu().numpy(), hkv, D)
-    return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    # The same bytes moved by a plain device copy (torch's copy kernel), timed the same
+    # way: the practical ceiling for a transfer this small on this part.
+    valid = n - 128
+    srcs = [torch.randn(2, valid, hkv * D, generator=dg, device=dev, dtype=torch.bfloat16)
+            for _ in range(len(sets))]
+    dsts = [torch.empty_like(x) for x in srcs]
+    for x, y in zip(srcs, dsts):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    cgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cgraph):
+        for x, y in zip(srcs, dsts):
+            y.copy_(x)
+    copy_ms = time_launches(cgraph.replay, replays, max(1, warmup // len(sets))) / len(srcs)
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6, copy_ms=copy_ms)
 
 
 LAYER_TOKENS = 16384  # one full prefill step of the engine (max_num_batched_tokens)
@@ -310,6 +324,7 @@ def run_extras(dev, steps: int, warmup: int) -> dict:
     a = bench_append(dev, *n["append"])
     extras["kv_append"] = dict(gbs=round(a["gbs"], 1), frac=round(a["gbs"] / HBM_PEAK_GBS, 4),
                                us=round(a["ms"] * 1e3, 3), bytes=a["bytes"],
+                               same_bytes_device_copy_us=round(a["copy_ms"] * 1e3, 3),
                                workload="4096 tok x 8 kv heads x 128 bf16, 3968 valid + 128 pad slots, "
                                         "cache [512,256,8,128], 24 rotating input sets, graph-replayed")
     torch.cuda.empty_cache()
