@@ -211,3 +211,39 @@ def test_decode_golden(cuda_device):
     torch.testing.assert_close(out.cpu().double(), torch.from_numpy(f["out"]), **TOL)
     # one-token row: exactly the V row
     assert np.array_equal(out[0].cpu().float().numpy(), f["out"][0].astype(np.float32))
+
+
+def test_decode_one_long_sequence_spans_the_grid(cuda_device):
+    """A single 32k-token context (plus a 1-token one): the stream-K split cuts it into
+    many ranges across the whole grid and the merge combines them."""
+    g = gen(31)
+    ctx = torch.tensor([32768, 1], dtype=torch.int32)
+    nb = 128 + 1 + 3
+    _, kc, vc = interleaved_pool(nb, 256, 8, 128, g)
+    bt = random_block_tables([32768, 1], 256, nb, g)
+    q = randn_bf16((2, 16, 128), g)
+    _check(cuda_device, q, kc, vc, bt, ctx)
+
+
+def test_decode_batch_above_one_launch(cuda_device):
+    """More sequences than one launch's prefix-sum table holds (4096): the host splits
+    the batch into consecutive launches that share the workspace."""
+    B = 4100
+    q, kc, vc, bt, ctx = _case(32, B=B, hq=4, hkv=2, bs=64, lo=0, hi=70)
+    _check(cuda_device, q, kc, vc, bt, ctx)
+
+
+def test_decode_block_size_512_and_strided_query(cuda_device):
+    """512-token pages, and q given as a strided view of the fused qkv rows (row stride
+    (Hq + 2 Hkv) * D, as the model produces it)."""
+    hq, hkv, B = 8, 4, 6
+    q0, kc, vc, bt, ctx = _case(33, B=B, hq=hq, hkv=hkv, bs=512, lo=1, hi=3000)
+    g = gen(34)
+    qkv = randn_bf16((B, (hq + 2 * hkv) * 128), g)
+    qkv[:, :hq * 128] = q0.reshape(B, -1)
+    qv = qkv[:, :hq * 128].view(B, hq, 128)
+    assert qv.stride(0) == (hq + 2 * hkv) * 128
+    d = cuda_device
+    out = _decode(qkv.to(d)[:, :hq * 128].view(B, hq, 128), kc.to(d), vc.to(d), ctx.to(d), bt.to(d))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), ref.paged_decode(q0, kc, vc, bt, ctx, SCALE), **TOL)

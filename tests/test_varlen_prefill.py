@@ -194,3 +194,42 @@ def test_prefill_golden(cuda_device):
                    scale=float(f["scale"]), bt=torch.from_numpy(f["block_tables"]).to(d))
     torch.cuda.synchronize()
     torch.testing.assert_close(out.cpu().double(), torch.from_numpy(f["out"]), **TOL)
+
+
+def test_paged_table_longer_than_64_blocks(cuda_device):
+    """A context of more than 64 blocks: the first 64 block ids come from registers, the
+    rest from the table in memory (64-token pages, klen 4800 = 75 blocks)."""
+    qlens = [300, 40]
+    prefix = [4500, 4200]
+    q, kc, vc, bt, cq, ck = _paged_case(250, qlens, prefix, 4, 2, 64)
+    assert bt.shape[1] >= 75
+    d = cuda_device
+    out = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
+    torch.cuda.synchronize()
+    want = ref.varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt)
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
+
+
+def test_paged_block_size_512(cuda_device):
+    qlens = [700, 3, 513]
+    prefix = [512, 1000, 0]
+    q, kc, vc, bt, cq, ck = _paged_case(251, qlens, prefix, 16, 8, 512)
+    d = cuda_device
+    out = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
+    torch.cuda.synchronize()
+    want = ref.varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt)
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
+
+
+def test_many_sequences_and_query_tile_pairs(cuda_device):
+    """Many short sequences and an odd number of query tiles per sequence: the grid pads
+    to whole pairs of tiles on every XCD and the extra work items do nothing."""
+    g = gen(252)
+    qlens = [int(x) for x in torch.randint(1, 200, (67,), generator=g)]
+    prefix = [int(x) * 64 for x in torch.randint(0, 5, (67,), generator=g)]
+    q, kc, vc, bt, cq, ck = _paged_case(253, qlens, prefix, 8, 4, 64)
+    d = cuda_device
+    out = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
+    torch.cuda.synchronize()
+    want = ref.varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt)
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
