@@ -266,6 +266,73 @@ def bench_prefill(dev, steps, warmup):
     return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9)
 
 
+def _median_runs(fn, budget_s: float, min_runs: int = 3, max_runs: int = 50) -> tuple[float, int]:
+    fn()  # warm-up
+    times, t_end = [], time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_append(budget_s: float = 8.0):
+    """The oracle's PyTorch-eager index-put on the host cores, whole config A."""
+    from oracle.kvpath_oracle import append_bytes, torch_append
+
+    n, hkv, nb = 4096, 8, 512
+    g = torch.Generator().manual_seed(0)
+    kc = torch.randn(nb, BS, hkv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, BS, hkv, D, generator=g).to(torch.bfloat16)
+    key = torch.randn(n, hkv, D, generator=g).to(torch.bfloat16)
+    value = torch.randn(n, hkv, D, generator=g).to(torch.bfloat16)
+    slots = torch.cat([torch.randperm(nb * BS, generator=g)[:n - 128].to(torch.int32),
+                       torch.full((128,), -1, dtype=torch.int32)])
+    sec, runs = _median_runs(lambda: torch_append(key, value, kc, vc, slots), budget_s)
+    nbytes = append_bytes(slots.numpy(), hkv, D)
+    return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"whole workload (4096 tokens, 128 padding), torch {torch.__version__} index-put, "
+                       f"median of {runs} runs")
+
+
+def cpu_baseline_prefill(budget_s: float = 15.0, nseq: int = 4):
+    """The oracle's per-sequence gather + masked bf16 SDPA on the host cores, over the
+    first sequences of the prefix-cached prefill workload."""
+    from oracle.kvpath_oracle import prefill_flops, sdpa_varlen_prefill
+
+    g = torch.Generator().manual_seed(0)
+    hq, hkv, nb = 16, 8, 4096
+    perm = torch.randperm(nb, generator=g).tolist()
+    qlens, klens, tables, pos = [], [], [], 0
+    for _ in range(8):  # the same draws as bench_prefill
+        p = 256 * int(torch.randint(0, 17, (1,), generator=g))
+        shared = perm[pos:pos + p // BS]
+        pos += p // BS
+        for _ in range(4):
+            n = int(torch.randint(100, 1025, (1,), generator=g))
+            own = perm[pos:pos + math.ceil((p + n) / BS) - len(shared)]
+            pos += len(own)
+            qlens.append(n)
+            klens.append(p + n)
+            tables.append(shared + own)
+    qlens, klens, tables = qlens[:nseq], klens[:nseq], tables[:nseq]
+    ids = sorted({b for t in tables for b in t})
+    remap = {b: i for i, b in enumerate(ids)}
+    width = max(len(t) for t in tables)
+    bt = torch.tensor([[remap[b] for b in t] + [-1] * (width - len(t)) for t in tables], dtype=torch.int32)
+    kc = torch.randn(len(ids), BS, hkv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(len(ids), BS, hkv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(sum(qlens), hq, D, generator=g).to(torch.bfloat16)
+    cq = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0)), dtype=torch.int32)
+    ck = torch.tensor([0] + list(torch.tensor(klens).cumsum(0)), dtype=torch.int32)
+    sec, runs = _median_runs(lambda: sdpa_varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt), budget_s)
+    flops = prefill_flops(cq.tolist(), ck.tolist(), hq, D)
+    return dict(value=round(flops / sec / 1e12, 4), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"first {nseq} of 32 sequences ({sum(qlens)} query tokens, {sum(klens)} keys), "
+                       f"torch {torch.__version__} bf16 SDPA with an explicit bottom-right mask, "
+                       f"median of {runs} runs")
+
+
 def cpu_baseline_decode(inp, budget_s: float = 20.0):
     """The oracle's bf16 gather + SDPA (a PyTorch-eager port of the reference path) on the
     host cores, over the first sequences of the headline workload."""
@@ -629,6 +696,9 @@ def main() -> int:
     if not args.no_extras:
         extras.update(run_extras(dev, args.steps, args.warmup))
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(inp)
+    if not args.no_cpu_baseline and not args.no_extras:
+        extras["kv_append"]["cpu_baseline"] = cpu_baseline_append()
+        extras["varlen_prefill"]["cpu_baseline"] = cpu_baseline_prefill()
     if not args.no_e2e:
         del inp
         torch.cuda.empty_cache()

@@ -249,6 +249,18 @@ def sdpa_paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     return out
 
 
+def torch_append(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 slot_mapping: torch.Tensor) -> None:
+    """Timed CPU baseline of the append: PyTorch-eager index-put of the valid rows into
+    the caches viewed as [num_blocks * block_size, Hkv * D] rows (block-stride aware)."""
+    valid = slot_mapping >= 0
+    slots = slot_mapping[valid].long()
+    bs = k_cache.shape[1]
+    for cache, src in ((k_cache, key), (v_cache, value)):
+        rows = cache.reshape(cache.shape[0], bs, -1)
+        rows[slots // bs, slots % bs] = src[valid].reshape(int(valid.sum()), -1)
+
+
 def sdpa_varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, block_tables=None) -> torch.Tensor:
     """Timed CPU baseline of varlen prefill: per-sequence gather + masked SDPA."""
     out = torch.zeros_like(q)
