@@ -393,24 +393,53 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 // Combines the per-range partial states of sequences that span several ranges.
 // grid = (ceil(num_q_heads / 8), num_seqs), 1024 threads: 8 query heads x 128 dims,
 // one output element per thread (few, large workgroups: dispatch is the main cost).
+// The kernel is latency-bound: the first kSpecParts partial rows are loaded together
+// with the header words (their addresses do not depend on the part count), so the
+// common case costs one memory round trip; rows past the part count are ignored.
 constexpr int kMergeHeads = 8;
+constexpr int kSpecParts = 4;
 __global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_kernel(const DecodeParams p) {
   constexpr int D = kDecodeHeadDim;
   const int h = blockIdx.x * kMergeHeads + static_cast<int>(threadIdx.x) / D;
   const int b = blockIdx.y;
   const int d = threadIdx.x % D;
   if (h >= p.num_q_heads) return;
-  const int cb = p.header[kHeaderInts + b], cb1 = p.header[kHeaderInts + b + 1];
-  if (cb1 <= cb) return;  // no steps: written by the main kernel
-  const int np = num_parts(cb, cb1, p.header[0]);
-  if (np <= 1) return;  // written by the main kernel
   const int64_t row0 = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.max_parts;
   const float* ml = p.part_ml + row0 * 2;
   const float* po = p.part_o + row0 * D + d;
-  // Batches of 8 parts: all loads of a batch are issued before any is used, so the
-  // common case (<= 8 parts) costs one memory round trip after the header.
-  float mm = kMaxFloor, ll = 0.f, oo = 0.f;
-  for (int s0 = 0; s0 < np; s0 += 8) {
+  float2 st0[kSpecParts];
+  float ov0[kSpecParts];
+#pragma unroll
+  for (int k = 0; k < kSpecParts; ++k) {
+    const int s = min(k, p.max_parts - 1);
+    st0[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
+    ov0[k] = po[static_cast<int64_t>(s) * D];
+  }
+  const int cb = p.header[kHeaderInts + b], cb1 = p.header[kHeaderInts + b + 1];
+  const int spr = p.header[0];
+  // Consumes the rows here, before the branches below, so the compiler cannot sink their
+  // loads under them: rows and header are then in flight together.
+#pragma unroll
+  for (int k = 0; k < kSpecParts; ++k) asm volatile("" ::"v"(st0[k].x), "v"(st0[k].y), "v"(ov0[k]));
+  asm volatile("" ::"s"(spr));
+  if (cb1 <= cb) return;  // no steps: written by the main kernel
+  const int np = num_parts(cb, cb1, spr);
+  if (np <= 1) return;  // written by the main kernel
+  float mm = kMaxFloor;
+#pragma unroll
+  for (int k = 0; k < kSpecParts; ++k)
+    if (k < np) mm = fmaxf(mm, st0[k].x);
+  float ll = 0.f, oo = 0.f;
+#pragma unroll
+  for (int k = 0; k < kSpecParts; ++k) {
+    if (k < np) {
+      const float w = fast_exp2(st0[k].x - mm);
+      ll += w * st0[k].y;
+      oo += w * ov0[k];
+    }
+  }
+  // Further parts (long sequences): batches of 8, all loads of a batch issued first.
+  for (int s0 = kSpecParts; s0 < np; s0 += 8) {
     float2 st[8];
     float ov[8];
 #pragma unroll

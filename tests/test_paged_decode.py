@@ -247,3 +247,15 @@ def test_decode_block_size_512_and_strided_query(cuda_device):
     out = _decode(qkv.to(d)[:, :hq * 128].view(B, hq, 128), kc.to(d), vc.to(d), ctx.to(d), bt.to(d))
     torch.cuda.synchronize()
     torch.testing.assert_close(out.cpu().float(), ref.paged_decode(q0, kc, vc, bt, ctx, SCALE), **TOL)
+
+
+def test_decode_back_to_back_shapes_share_the_workspace(cuda_device):
+    """Back-to-back calls of different shapes on the one per-device workspace (each
+    later call laying its partial states over an earlier call's) all match the oracle.
+    The cases cover every GQA ratio and sequences cut into many parts."""
+    d = cuda_device
+    cases = [(40, 8, 1, 64, 4000, 9000), (3, 64, 8, 256, 20000, 30000), (64, 16, 8, 256, 1, 2048),
+             (7, 8, 2, 128, 900, 5000), (5, 16, 4, 64, 3000, 7000)]
+    for i, (B, hq, hkv, bs, lo, hi) in enumerate(cases):
+        q, kc, vc, bt, ctx = _case(40 + i, B=B, hq=hq, hkv=hkv, bs=bs, lo=lo, hi=hi)
+        _check(d, q, kc, vc, bt, ctx)
