@@ -45,6 +45,38 @@ BS, D = 256, 128
 SCALE = D ** -0.5
 
 
+# ----------------------------------------------------------------------------- units
+
+def decode_bytes(context_lens, num_q_heads: int, num_kv_heads: int, head_dim: int, block_size: int) -> int:
+    """Algorithmic HBM bytes of one paged-decode call: each cached K and V element once
+    (bf16), q read and o written once, plus context_lens and the block-table entries used."""
+    ctx = [int(c) for c in context_lens]
+    kv_row = num_kv_heads * head_dim * 2
+    blocks = sum(-(-c // block_size) for c in ctx)
+    return 2 * kv_row * sum(ctx) + 2 * len(ctx) * num_q_heads * head_dim * 2 + 4 * (len(ctx) + blocks)
+
+
+def append_bytes(slot_mapping, num_kv_heads: int, head_dim: int) -> int:
+    """Algorithmic HBM bytes of one KV append: K and V of each valid (non-negative) slot
+    read once and written once (bf16), plus the int32 slot_mapping."""
+    slots = [int(x) for x in slot_mapping]
+    valid = sum(1 for x in slots if x >= 0)
+    return 4 * valid * num_kv_heads * head_dim * 2 + 4 * len(slots)
+
+
+def prefill_flops(cu_seqlens_q, cu_seqlens_k, num_q_heads: int, head_dim: int) -> int:
+    """Algorithmic flops of bottom-right causal varlen prefill: 4 * Hq * D per unmasked
+    (query, key) pair.  A sequence with n queries and k >= n keys has n*k - n(n-1)/2
+    such pairs (query i sees k - n + 1 + i keys); with k < n only the last k queries see
+    any key, k(k+1)/2 pairs."""
+    pairs = 0
+    for s in range(len(cu_seqlens_q) - 1):
+        n = int(cu_seqlens_q[s + 1]) - int(cu_seqlens_q[s])
+        k = int(cu_seqlens_k[s + 1]) - int(cu_seqlens_k[s])
+        pairs += n * k - n * (n - 1) // 2 if k >= n else k * (k + 1) // 2
+    return 4 * num_q_heads * head_dim * pairs
+
+
 # ----------------------------------------------------------------------------- inputs
 
 def decode_inputs(dev, B, hq, hkv, lo, hi, pool_blocks, seed=0):
@@ -84,8 +116,6 @@ def time_launches(fn, steps: int, warmup: int):
 
 def bench_decode(dev, steps, warmup, shape):
     from kavor_amd.layers.attention import paged_decode, reserve_decode_workspace
-    from oracle.kvpath_oracle import decode_bytes
-
     if shape == "qwen3_0.6b":
         inp = decode_inputs(dev, 256, 16, 8, 100, 2048, 4096)
     else:
@@ -104,7 +134,6 @@ def bench_decode(dev, steps, warmup, shape):
 
 def bench_append(dev, steps, warmup):
     from kavor_amd.layers.attention import store_kvcache
-    from oracle.kvpath_oracle import append_bytes
 
     n, hkv, nb = 4096, 8, 512
     g = torch.Generator().manual_seed(0)
@@ -130,7 +159,22 @@ def bench_append(dev, steps, warmup):
             store_kvcache(k, v, kc, vc, s)
     replays = max(2, (steps if steps < 16 else max(steps, 48)) // len(sets))
     ms = time_launches(graph.replay, replays, max(1, warmup // len(sets))) / len(sets)
-    nbytes = append_bytes(sets[0][2].cpu().numpy(), hkv, D)
+    nbytes = append_bytes(sets[0][2].cpu().tolist(), hkv, D)
+    # The engine's layout: one 1 MiB page per block holding K then V (block stride
+    # 2 * 256 * 8 * 128 elements), as the page pool binds it.
+    page = 2 * BS * hkv * D
+    pool = torch.randn(nb, page, generator=dg, device=dev, dtype=torch.bfloat16)
+    kp = pool.as_strided((nb, BS, hkv, D), (page, hkv * D, D, 1), 0)
+    vp = pool.as_strided((nb, BS, hkv, D), (page, hkv * D, D, 1), BS * hkv * D)
+    for k, v, s in sets:
+        store_kvcache(k, v, kp, vp, s)
+    torch.cuda.synchronize()
+    pgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(pgraph):
+        for k, v, s in sets:
+            store_kvcache(k, v, kp, vp, s)
+    paged_ms = time_launches(pgraph.replay, replays, max(1, warmup // len(sets))) / len(sets)
+    del pgraph, pool, kp, vp
     # The same bytes moved by a plain device copy (torch's copy kernel), timed the same
     # way: the practical ceiling for a transfer this small on this part.
     valid = n - 128
@@ -145,7 +189,7 @@ def bench_append(dev, steps, warmup):
         for x, y in zip(srcs, dsts):
             y.copy_(x)
     copy_ms = time_launches(cgraph.replay, replays, max(1, warmup // len(sets))) / len(srcs)
-    return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6, copy_ms=copy_ms)
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6, copy_ms=copy_ms, paged_ms=paged_ms)
 
 
 LAYER_TOKENS = 16384  # one full prefill step of the engine (max_num_batched_tokens)
@@ -231,8 +275,6 @@ def bench_layers(dev, steps, warmup):
 
 def bench_prefill(dev, steps, warmup):
     from kavor_amd.layers.attention import varlen_prefill
-    from oracle.kvpath_oracle import prefill_flops
-
     g = torch.Generator().manual_seed(0)
     hq, hkv, nb = 16, 8, 4096
     perm = torch.randperm(nb, generator=g).tolist()
@@ -278,7 +320,7 @@ def _median_runs(fn, budget_s: float, min_runs: int = 3, max_runs: int = 50) -> 
 
 def cpu_baseline_append(budget_s: float = 8.0):
     """The oracle's PyTorch-eager index-put on the host cores, whole config A."""
-    from oracle.kvpath_oracle import append_bytes, torch_append
+    from oracle.kvpath_oracle import torch_append
 
     n, hkv, nb = 4096, 8, 512
     g = torch.Generator().manual_seed(0)
@@ -289,7 +331,7 @@ def cpu_baseline_append(budget_s: float = 8.0):
     slots = torch.cat([torch.randperm(nb * BS, generator=g)[:n - 128].to(torch.int32),
                        torch.full((128,), -1, dtype=torch.int32)])
     sec, runs = _median_runs(lambda: torch_append(key, value, kc, vc, slots), budget_s)
-    nbytes = append_bytes(slots.numpy(), hkv, D)
+    nbytes = append_bytes(slots.tolist(), hkv, D)
     return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
                 sample=f"whole workload (4096 tokens, 128 padding), torch {torch.__version__} index-put, "
                        f"median of {runs} runs")
@@ -298,7 +340,7 @@ def cpu_baseline_append(budget_s: float = 8.0):
 def cpu_baseline_prefill(budget_s: float = 15.0, nseq: int = 4):
     """The oracle's per-sequence gather + masked bf16 SDPA on the host cores, over the
     first sequences of the prefix-cached prefill workload."""
-    from oracle.kvpath_oracle import prefill_flops, sdpa_varlen_prefill
+    from oracle.kvpath_oracle import sdpa_varlen_prefill
 
     g = torch.Generator().manual_seed(0)
     hq, hkv, nb = 16, 8, 4096
@@ -333,12 +375,12 @@ def cpu_baseline_prefill(budget_s: float = 15.0, nseq: int = 4):
                        f"median of {runs} runs")
 
 
-def cpu_baseline_decode(inp, budget_s: float = 20.0):
+def cpu_baseline_decode(inp, budget_s: float = 20.0, nseq: int = 32):
     """The oracle's bf16 gather + SDPA (a PyTorch-eager port of the reference path) on the
-    host cores, over the first sequences of the headline workload."""
-    from oracle.kvpath_oracle import sdpa_paged_decode, decode_bytes
+    host cores, over the first `nseq` sequences of a decode workload."""
+    from oracle.kvpath_oracle import sdpa_paged_decode
 
-    nseq = 32  # torch keeps its default thread count (OMP_NUM_THREADS, the host's CPU share)
+    # torch keeps its default thread count (OMP_NUM_THREADS, the host's CPU share)
     ctx = inp["ctx_host"][:nseq]
     bt = inp["bt_host"][:nseq]
     ids = sorted({int(x) for x in bt.flatten() if x >= 0})
@@ -359,9 +401,78 @@ def cpu_baseline_decode(inp, budget_s: float = 20.0):
     nbytes = decode_bytes(ctx.tolist(), inp["hq"], inp["hkv"], D, BS)
     return dict(value=round(nbytes / sec / 1e9, 4), unit="GB/s", cores=torch.get_num_threads(),
                 kind="port",
-                sample=f"first {nseq} of 256 sequences ({int(ctx.sum())} cached tokens), "
+                sample=f"first {nseq} of {inp['q'].shape[0]} sequences ({int(ctx.sum())} cached tokens), "
                        f"torch {torch.__version__} bf16 SDPA on {platform.processor() or platform.machine()}, "
                        f"median of {len(times)} runs")
+
+
+def cpu_baseline_e2e(nseq: int = 16, steps: int = 3):
+    """A fixed window of the end-to-end workload on the host cores: greedy decode steps
+    of the Qwen3-0.6B architecture for the first `nseq` requests, their caches at the
+    prompt lengths, computed with the oracle's layer restatements, its PyTorch-eager
+    index-put append and its bf16 gather + SDPA attention.  The weights are the engine's
+    own (initialised on the GPU with the engine's seed, then copied to the host).
+    Returns decode tok/s over the window (comparable to decode_tok_s)."""
+    import torch.nn.functional as F
+
+    from kavor_amd.engine.qwen3 import Qwen3ForCausalLM, Qwen3Spec
+    from oracle import layers_oracle as L
+    from oracle.kvpath_oracle import sdpa_paged_decode, torch_append
+
+    spec = Qwen3Spec()
+    model = Qwen3ForCausalLM(spec, "cuda")
+    model.init_random(0)
+    model = model.to("cpu")
+    torch.cuda.empty_cache()
+    eps, hq, hkv = spec.rms_norm_eps, spec.num_attention_heads, spec.num_key_value_heads
+    prompts, _ = e2e_workload()
+    ctx = torch.tensor([len(p) for p in prompts[:nseq]], dtype=torch.int32)
+    nblk = [math.ceil((int(c) + steps + 1) / BS) for c in ctx]
+    width = max(nblk)
+    bt = torch.full((nseq, width), -1, dtype=torch.int32)
+    first = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = torch.arange(first, first + n, dtype=torch.int32)
+        first += n
+    g = torch.Generator().manual_seed(0)
+    caches = [tuple((torch.randn(first, BS, hkv, D, generator=g) * 0.5).to(torch.bfloat16) for _ in range(2))
+              for _ in range(spec.num_hidden_layers)]
+    rows = torch.arange(nseq)
+
+    @torch.inference_mode()
+    def decode_step(ids, ctx):
+        pos = ctx.long()
+        slots = (bt[rows, pos // BS].long() * BS + pos % BS).to(torch.int32)
+        h, residual = F.embedding(ids, model.embed_tokens), None
+        for layer, (kc, vc) in zip(model.layers, caches):
+            if residual is None:
+                x, residual = L.rms_norm(h, layer.input_layernorm.weight, eps), h
+            else:
+                x, residual = L.add_rms_norm(h, residual, layer.input_layernorm.weight, eps)
+            a = layer.self_attn
+            q, k, v = L.qk_norm_rope(F.linear(x, a.qkv_proj), pos, model.rope_table, a.q_norm.weight,
+                                     a.k_norm.weight, eps, hq, hkv)
+            torch_append(k, v, kc, vc, slots)
+            o = sdpa_paged_decode(q, kc, vc, bt, ctx + 1, D ** -0.5)
+            x, residual = L.add_rms_norm(F.linear(o.reshape(nseq, -1), a.o_proj), residual,
+                                         layer.post_attention_layernorm.weight, eps)
+            h = F.linear(L.silu_and_mul(F.linear(x, layer.mlp.gate_up_proj)), layer.mlp.down_proj)
+        x, _ = L.add_rms_norm(h, residual, model.norm.weight, eps)
+        return L.greedy(F.linear(x, model.lm_head)), ctx + 1
+
+    ids = torch.tensor([p[-1] for p in prompts[:nseq]], dtype=torch.int64)
+    ids, ctx = decode_step(ids, ctx)  # warm-up step
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ids, ctx = decode_step(ids, ctx)
+    sec = time.perf_counter() - t0
+    return dict(value=round(nseq * steps / sec, 2), unit="decode tok/s", cores=torch.get_num_threads(),
+                kind="port",
+                sample=f"{steps} greedy decode steps (after 1 warm-up) of the first {nseq} of 256 requests, "
+                       f"engine weights, "
+                       f"caches at their prompt lengths ({int(ctx.sum()) - nseq * (steps + 1)} tokens); "
+                       f"oracle layers + index-put append + bf16 gather/SDPA attention, torch "
+                       f"{torch.__version__}")
 
 
 def load_traffic(name: str):
@@ -385,15 +496,18 @@ def extra_counts(steps: int, warmup: int) -> dict:
                 decode_8b=(max(20, steps // 4), max(5, warmup // 6)))
 
 
-def run_extras(dev, steps: int, warmup: int) -> dict:
+def run_extras(dev, steps: int, warmup: int, cpu_baseline: bool = False) -> dict:
     n = extra_counts(steps, warmup)
     extras = {}
     a = bench_append(dev, *n["append"])
     extras["kv_append"] = dict(gbs=round(a["gbs"], 1), frac=round(a["gbs"] / HBM_PEAK_GBS, 4),
                                us=round(a["ms"] * 1e3, 3), bytes=a["bytes"],
                                same_bytes_device_copy_us=round(a["copy_ms"] * 1e3, 3),
+                               page_interleaved=dict(us=round(a["paged_ms"] * 1e3, 3),
+                                                     gbs=round(a["bytes"] / a["paged_ms"] / 1e6, 1)),
                                workload="4096 tok x 8 kv heads x 128 bf16, 3968 valid + 128 pad slots, "
-                                        "cache [512,256,8,128], 24 rotating input sets, graph-replayed")
+                                        "cache [512,256,8,128] (page_interleaved: the engine's K/V-per-"
+                                        "page pool, block stride 2x), 24 rotating input sets, graph-replayed")
     torch.cuda.empty_cache()
     p = bench_prefill(dev, *n["prefill"])
     extras["varlen_prefill"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
@@ -402,10 +516,13 @@ def run_extras(dev, steps: int, warmup: int) -> dict:
     torch.cuda.empty_cache()
     extras["layer_kernels"] = bench_layers(dev, *n["layers"])
     torch.cuda.empty_cache()
-    _, c = bench_decode(dev, *n["decode_8b"], "qwen3_8b")
+    inp8, c = bench_decode(dev, *n["decode_8b"], "qwen3_8b")
     extras["paged_decode_qwen3_8b"] = dict(gbs=round(c["gbs"], 1), frac=round(c["gbs"] / HBM_PEAK_GBS, 4),
                                            ms=round(c["ms"], 4), bytes=c["bytes"],
                                            workload="B=128, 32q/8kv, ctx U[1024,32768], pool 20000 blocks")
+    if cpu_baseline:
+        extras["paged_decode_qwen3_8b"]["cpu_baseline"] = cpu_baseline_decode(inp8, budget_s=10.0, nseq=4)
+    del inp8
     torch.cuda.empty_cache()
     return extras
 
@@ -435,6 +552,106 @@ PROFILE_CMDS = [
     "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_write -o run -- python $R/bench.py --profile",
     "python $R/bench.py --summarize $R/gpurun_out/pmc_trace $R/gpurun_out/pmc_fetch $R/gpurun_out/pmc_write",
 ]
+
+PREFILL_PMC_PASSES = [
+    "SQ_VALU_MFMA_BUSY_CYCLES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA "
+    "SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE",
+    "SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_MISC "
+    "SQ_INSTS_LDS SQ_CYCLES SQ_WAIT_INST_LDS GRBM_GUI_ACTIVE",
+]
+PREFILL_PMC_CMDS = [
+    "cd /tmp && export TMPDIR=/tmp",
+    "rocprofv3 --pmc " + PREFILL_PMC_PASSES[0] + " --output-format csv -d $R/gpurun_out/ppmc_a -o run -- "
+    "python $R/bench.py --profile-prefill",
+    "rocprofv3 --pmc " + PREFILL_PMC_PASSES[1] + " --output-format csv -d $R/gpurun_out/ppmc_b -o run -- "
+    "python $R/bench.py --profile-prefill",
+    "python $R/bench.py --summarize-prefill-pmc $R/gpurun_out/ppmc_a $R/gpurun_out/ppmc_b",
+]
+
+
+def summarize_prefill_pmc(dir_a: str, dir_b: str) -> int:
+    """profiles/varlen_prefill_prefix_32seq_pmc.md: where the prefill kernel's cycles go,
+    from two rocprofv3 --pmc passes over --profile-prefill (medians over the dispatches
+    after the first third).  Counters are summed over the device; GRBM_GUI_ACTIVE counts
+    once per XCD, so one XCD's busy cycles are its sum divided by the XCD count."""
+    import csv
+    from collections import defaultdict
+
+    name = "void kvp::varlen_prefill_kernel<2, true, true>"
+    vals = defaultdict(lambda: defaultdict(float))
+    agent = {}
+    for d in (dir_a, dir_b):
+        for r in csv.DictReader(open(Path(d) / "run_counter_collection.csv")):
+            if r["Kernel_Name"].startswith(name):
+                vals[(d, int(r["Dispatch_Id"]))][r["Counter_Name"]] += float(r["Counter_Value"])
+        for r in csv.DictReader(open(Path(d) / "run_agent_info.csv")):
+            if r.get("Name", "").startswith("gfx"):
+                agent = r
+    cus, simds, xcds = int(agent["Cu_Count"]), int(agent["Simd_Count"]), int(agent["Num_Xcc"])
+
+    def med(counter):
+        per = [v[counter] for (d, _), v in sorted(vals.items()) if counter in v]
+        per = per[len(per) // 3:]
+        return (statistics.median(per), len(per)) if per else (float("nan"), 0)
+
+    gui_a, n = med("GRBM_GUI_ACTIVE")
+    xcd_cycles = gui_a / xcds
+    mfma_busy = med("SQ_VALU_MFMA_BUSY_CYCLES")[0] / (xcd_cycles * simds)
+    waves_per_simd = med("SQ_WAVE_CYCLES")[0] / xcd_cycles / cus
+    g = torch.Generator().manual_seed(0)
+    perm = torch.randperm(4096, generator=g).tolist()  # the bench_prefill draws
+    qlens, klens = [], []
+    for _ in range(8):
+        p = 256 * int(torch.randint(0, 17, (1,), generator=g))
+        for _ in range(4):
+            nq = int(torch.randint(100, 1025, (1,), generator=g))
+            qlens.append(nq)
+            klens.append(p + nq)
+    del perm
+    cq = [0] + list(torch.tensor(qlens).cumsum(0).tolist())
+    ck = [0] + list(torch.tensor(klens).cumsum(0).tolist())
+    algo = prefill_flops(cq, ck, 16, D)
+    mfma_flops = med("SQ_INSTS_VALU_MFMA_MOPS_BF16")[0] * 512
+    lds_conf = med("SQ_LDS_BANK_CONFLICT")[0] / max(1.0, med("SQ_LDS_IDX_ACTIVE")[0])
+    wave_cycles = med("SQ_WAVE_CYCLES")[0]
+    lines = [
+        f"# varlen_prefill_prefix_32seq counters: `{name}(kvp::PrefillParams)`",
+        "",
+        "Commands (from the repository root on the GPU host, `R=$PWD`):",
+        "",
+        "```",
+        *PREFILL_PMC_CMDS,
+        "```",
+        "",
+        f"Device: {agent.get('Name')} with {cus} CUs, {simds} SIMDs, {xcds} XCDs. Medians over the last {n} "
+        "of the profiled dispatches. GRBM_GUI_ACTIVE is summed over the XCDs, so one XCD's busy cycles "
+        f"= GRBM_GUI_ACTIVE / {xcds}.",
+        "",
+        "| Quantity | Value | From |",
+        "|---|---|---|",
+        f"| busy cycles per XCD | {xcd_cycles:,.0f} | GRBM_GUI_ACTIVE / {xcds} |",
+        f"| MFMA busy | {100 * mfma_busy:.1f}% of SIMD cycles | SQ_VALU_MFMA_BUSY_CYCLES / (cycles x {simds}) |",
+        f"| resident waves per SIMD | {waves_per_simd:.2f} of 2 (VGPR-bound occupancy) | "
+        f"SQ_WAVE_CYCLES / cycles / {cus} |",
+        f"| MFMA flops executed | {mfma_flops:.4g} = {mfma_flops / algo:.2f} x the algorithmic {algo:.4g} "
+        "(the rest: masked halves of diagonal tiles, padded rows of the last query tile) | "
+        "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 |",
+        f"| VALU / MFMA / LDS instructions | {med('SQ_INSTS_VALU')[0]:,.0f} / {med('SQ_INSTS_MFMA')[0]:,.0f} / "
+        f"{med('SQ_INSTS_LDS')[0]:,.0f} | SQ_INSTS_VALU, SQ_INSTS_MFMA, SQ_INSTS_LDS |",
+        f"| LDS bank-conflict cycles | {100 * lds_conf:.1f}% of LDS active cycles | "
+        "SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE |",
+        f"| waves waiting on a dependency | {100 * med('SQ_WAIT_INST_ANY')[0] / wave_cycles:.1f}% of wave cycles "
+        f"(LDS: {100 * med('SQ_WAIT_INST_LDS')[0] / wave_cycles:.1f}%) | SQ_WAIT_INST_ANY, SQ_WAIT_INST_LDS "
+        "/ SQ_WAVE_CYCLES |",
+        f"| VALU / LDS issue | {100 * med('SQ_ACTIVE_INST_VALU')[0] / wave_cycles:.1f}% / "
+        f"{100 * med('SQ_ACTIVE_INST_LDS')[0] / wave_cycles:.1f}% of wave cycles | SQ_ACTIVE_INST_VALU, "
+        "SQ_ACTIVE_INST_LDS / SQ_WAVE_CYCLES |",
+    ]
+    out = ROOT / "profiles" / "varlen_prefill_prefix_32seq_pmc.md"
+    out.write_text("\n".join(lines) + "\n")
+    print(f"wrote {out}", flush=True)
+    return 0
+
 
 # (profile file, kernel-name prefix, which occurrence group, algorithmic bytes or flops, unit)
 PROFILE_KERNELS = [
@@ -573,8 +790,6 @@ def summarize_e2e(trace_dir: str) -> int:
 
 
 def _decode_algo_bytes(B, hq, lo, hi, pool_blocks, seed=0):
-    from oracle.kvpath_oracle import decode_bytes
-
     g = torch.Generator().manual_seed(seed)
     ctx = torch.randint(lo, hi + 1, (B,), generator=g, dtype=torch.int32)
     return decode_bytes(ctx.tolist(), hq, 8, D, BS)
@@ -667,6 +882,10 @@ def main() -> int:
                     help="the default run's kernel launches without the CPU baseline and the engine, "
                          "for rocprofv3; starts with plain 1 GiB device copies used to calibrate "
                          "FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="only the prefix-cached prefill launches (30), for rocprofv3 --pmc passes")
+    ap.add_argument("--summarize-prefill-pmc", nargs=2, metavar=("PASS_A_DIR", "PASS_B_DIR"),
+                    help="write profiles/varlen_prefill_prefix_32seq_pmc.md from the two --pmc passes")
     ap.add_argument("--summarize-e2e", metavar="TRACE_DIR",
                     help="write profiles/e2e_qwen3_0.6b.md from rocprofv3 --stats over --e2e-only")
     args = ap.parse_args()
@@ -674,6 +893,8 @@ def main() -> int:
         return summarize_profiles(*args.summarize)
     if args.summarize_e2e:
         return summarize_e2e(args.summarize_e2e)
+    if args.summarize_prefill_pmc:
+        return summarize_prefill_pmc(*args.summarize_prefill_pmc)
     if args.gpus != 1:
         print(f"bench.py measures one GPU's paged KV-cache kernels; --gpus {args.gpus} is not "
               "supported (the path shards by kv head with no exchange inside attention).", file=sys.stderr)
@@ -687,6 +908,11 @@ def main() -> int:
     lib()
     if args.profile:
         return profile_run(dev, args.steps, args.warmup)
+    if args.profile_prefill:
+        bench_prefill(dev, 20, 10)
+        torch.cuda.synchronize()
+        print("prefill profile run done", flush=True)
+        return 0
     if args.e2e_only:
         print(json.dumps({"e2e_qwen3_0.6b": bench_e2e(args.e2e_seqs)}), flush=True)
         return 0
@@ -694,7 +920,7 @@ def main() -> int:
     inp, dec = bench_decode(dev, args.steps, args.warmup, "qwen3_0.6b")
     extras = {}
     if not args.no_extras:
-        extras.update(run_extras(dev, args.steps, args.warmup))
+        extras.update(run_extras(dev, args.steps, args.warmup, cpu_baseline=not args.no_cpu_baseline))
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(inp)
     if not args.no_cpu_baseline and not args.no_extras:
         extras["kv_append"]["cpu_baseline"] = cpu_baseline_append()
@@ -703,6 +929,8 @@ def main() -> int:
         del inp
         torch.cuda.empty_cache()
         extras["e2e_qwen3_0.6b"] = bench_e2e(args.e2e_seqs)
+        if not args.no_cpu_baseline:
+            extras["e2e_qwen3_0.6b"]["cpu_baseline"] = cpu_baseline_e2e()
 
     gbs = dec["gbs"]
     line = {
