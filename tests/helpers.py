@@ -68,3 +68,19 @@ def random_block_tables(context_lens: list[int], block_size: int, num_blocks: in
 def bits_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
     """Bitwise equality of two bf16 tensors (NaN payloads included)."""
     return torch.equal(a.contiguous().view(torch.int16), b.contiguous().view(torch.int16))
+
+
+def relocate_pages(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                   g: torch.Generator) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The same logical caches with every page moved to another physical block id: page p
+    becomes page perm[p], and the table entries are renumbered to match (padding kept)."""
+    nb = k_cache.shape[0]
+    perm = torch.randperm(nb, generator=g)
+    k2 = torch.empty_like(k_cache.contiguous())
+    v2 = torch.empty_like(v_cache.contiguous())
+    k2[perm] = k_cache
+    v2[perm] = v_cache
+    bt2 = block_tables.clone()
+    valid = bt2 >= 0
+    bt2[valid] = perm[bt2[valid].long()].to(torch.int32)
+    return k2, v2, bt2

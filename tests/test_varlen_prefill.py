@@ -8,7 +8,8 @@ import pytest
 import torch
 
 from oracle import kvpath_oracle as ref
-from tests.helpers import TOL, gen, randn_bf16, interleaved_pool, contiguous_caches, random_block_tables, bits_equal
+from tests.helpers import (TOL, gen, randn_bf16, interleaved_pool, contiguous_caches, random_block_tables,
+                           bits_equal, relocate_pages)
 from tests.test_golden import load, bf16
 
 pytestmark = pytest.mark.gpu
@@ -233,3 +234,15 @@ def test_many_sequences_and_query_tile_pairs(cuda_device):
     torch.cuda.synchronize()
     want = ref.varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt)
     torch.testing.assert_close(out.cpu().float(), want, **TOL)
+
+
+def test_paged_relocated_pages_are_bitwise_identical(cuda_device):
+    """Prefix-cached prefill over pages moved to other physical blocks (tables renumbered
+    to match) gives identical bits."""
+    qlens, prefix = [70, 300, 1, 129], [256, 37, 511, 0]
+    q, kc, vc, bt, cq, ck = _paged_case(230, qlens, prefix, 16, 8, 256)
+    k2, v2, bt2 = relocate_pages(kc, vc, bt, gen(231))
+    d = cuda_device
+    a = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d)).cpu()
+    b = _prefill(q.to(d), k2.to(d), v2.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt2.to(d)).cpu()
+    assert bits_equal(a, b)
