@@ -4,12 +4,16 @@
 // (kavor/layers/attention/flash_attention_kvcache.py:10-46): a pure bit copy of
 // num_kv_heads*head_dim bf16 values per tensor per token, slot -1 skipped.
 //
-// Mapping: one wave64 per token.  A token's K row and V row are cut into 16-byte
-// chunks (8 bf16); the wave's lanes own consecutive chunks, so every load and store
-// is a dwordx4 and a 16-lane group covers one 256-byte head row contiguously.  Each
-// lane issues all of its loads before its first store so a wave keeps up to 4 KiB in
-// flight; the token index, slot and row addresses are wave-uniform scalars.  For Qwen3
-// (8 kv heads x 128) a token row is 128 chunks per tensor: 2 K + 2 V chunks per lane.
+// Mapping: each wave64 moves two tokens.  A token's K row and V row are cut into
+// 16-byte chunks (8 bf16); the wave's lanes own consecutive chunks, so every load and
+// store is a dwordx4 and a 16-lane group covers one 256-byte head row contiguously.
+// Each lane issues the loads of both its tokens before it reads a slot or stores
+// anything, so a wave keeps 8 KiB in flight (Qwen3: 8 kv heads x 128 is 128 chunks per
+// tensor row, 2 K + 2 V chunks per lane per token).  Source rows are read once and
+// cache rows written once, so both go nontemporal.  Measured on the 4096-token append
+// (graph-replayed, rotating inputs): one token per wave 8.5 us; two 7.0 us; two with
+// nontemporal loads 6.6-6.7 us (60-61% of 8 TB/s); four or eight per wave 7.4 / 8.2 us
+// (too few waves); workgroups of 1-8 waves alike.
 #include "common.h"
 
 namespace kvp {
@@ -29,36 +33,28 @@ struct AppendParams {
   int32_t block_size;
 };
 
-constexpr int kAppendWaves = 4;  // tokens per workgroup
+constexpr int kAppendWaves = 4;
+constexpr int kAppendTokensPerWave = 2;
+constexpr int kAppendTokensPerGroup = kAppendWaves * kAppendTokensPerWave;
 
 // CPL = 16-byte chunks per lane per tensor: a token's K row and its V row are each
-// Hkv * HEAD_DIM / 8 chunks; lane l owns chunks l, l + 64, ... of both.  Every lane issues
-// all 2 * CPL loads before its first store; chunk indices are clamped onto the row's last
-// chunk, so neither loads nor stores need a branch.
+// Hkv * HEAD_DIM / 8 chunks; lane l owns chunks l, l + 64, ... of both (rows longer
+// than 64 * CPL chunks take several passes).  Chunk indices are clamped onto the row's
+// last chunk and token indices onto the last token, so no branch guards a load; a lane
+// past the row's end rewrites that chunk's bytes to the same place.
 template <int HEAD_DIM, int CPL>
 __global__ __launch_bounds__(64 * kAppendWaves) void kv_append_kernel(const AppendParams p) {
   constexpr int kChunksPerHead = HEAD_DIM / 8;
-  // Token index and slot are wave-uniform: keep them (and the address math) scalar.  No
-  // early return precedes the loads (the token index is clamped instead), so the only
-  // scalar round trip before them is the kernel-argument fetch.
+  constexpr int TPW = kAppendTokensPerWave;
+  // Token indices, slots and row addresses are wave-uniform.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tok_raw = blockIdx.x * kAppendWaves + wave;
-  const int tok = min(tok_raw, p.num_tokens - 1);
+  const int tok0 = (static_cast<int>(blockIdx.x) * kAppendWaves + wave) * TPW;
   const int lane = threadIdx.x & 63;
   const int cpt = p.num_kv_heads * kChunksPerHead;  // chunks per tensor row
-  const uint4* key_row = p.key + static_cast<int64_t>(tok) * p.key_tok_stride;
-  const uint4* value_row = p.value + static_cast<int64_t>(tok) * p.value_tok_stride;
-  const int32_t slot = p.slot_mapping[tok];
-  const bool store = tok_raw < p.num_tokens && slot >= 0 && static_cast<int64_t>(slot) < p.num_cache_slots;
-  const int32_t blk = slot / p.block_size;  // scalar division: no branch before the loads
-  const int32_t off = slot - blk * p.block_size;
-  const int64_t dst_base = static_cast<int64_t>(blk) * p.blk_stride + static_cast<int64_t>(off) * p.slot_stride;
 
   int j0 = 0;
   do {  // every row has at least one chunk group
-    uint4 kb[CPL], vb[CPL];
-    int64_t dofs[CPL];
-    int64_t kofs[CPL], vofs[CPL];
+    int64_t kofs[CPL], vofs[CPL], dofs[CPL];
 #pragma unroll
     for (int u = 0; u < CPL; ++u) {
       const int j = min(j0 + 64 * u + lane, cpt - 1);
@@ -68,20 +64,40 @@ __global__ __launch_bounds__(64 * kAppendWaves) void kv_append_kernel(const Appe
       vofs[u] = head * p.value_head_stride + part;
       dofs[u] = head * p.head_stride + part;
     }
-    // K row then V row (each a contiguous stretch of HBM), loads and stores alike.
+    uint4 kb[TPW][CPL], vb[TPW][CPL];
+    int32_t slots[TPW];
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) kb[u] = key_row[kofs[u]];
+    for (int q = 0; q < TPW; ++q) {
+      const int tok = min(tok0 + q, p.num_tokens - 1);
+      const uint4* key_row = p.key + static_cast<int64_t>(tok) * p.key_tok_stride;
+      const uint4* value_row = p.value + static_cast<int64_t>(tok) * p.value_tok_stride;
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) vb[u] = value_row[vofs[u]];
-    if (!store) return;  // -1 (padding), a slot outside the pool, or past the last token
-    // Cache rows are written once and read by a later kernel: nontemporal stores keep
-    // them out of L2 (measured 10.0 -> 8.3 us for 4096 tokens).  A lane past the row's
-    // last chunk was clamped onto that chunk and rewrites the same bytes to the same
-    // place, so the stores need no mask either.
+      for (int u = 0; u < CPL; ++u) kb[q][u] = load16_nt(key_row + kofs[u]);
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) store16_nt(p.k_cache + dst_base + dofs[u], kb[u]);
+      for (int u = 0; u < CPL; ++u) vb[q][u] = load16_nt(value_row + vofs[u]);
+      // Each token's slot is read after its rows are issued: without this fence the
+      // compiler hoists the slot loads, their wait and the division ahead of the row
+      // loads, and every wave pays a memory round trip before its first row load.  In
+      // this order the first token's stores can start while the second token's loads
+      // are still in flight.  (Reading the slots first, as scalar loads, measured 7.7 us.)
+      asm volatile("" ::: "memory");
+      slots[q] = p.slot_mapping[tok];
+    }
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) store16_nt(p.v_cache + dst_base + dofs[u], vb[u]);
+    for (int q = 0; q < TPW; ++q) {
+      const int tok = tok0 + q;
+      const int32_t slot = slots[q];
+      // -1 (padding), a slot outside the pool and tokens past the last are skipped; cache
+      // rows are written once and read by a later kernel, so the stores are nontemporal
+      if (tok >= p.num_tokens || slot < 0 || static_cast<int64_t>(slot) >= p.num_cache_slots) continue;
+      const int32_t blk = slot / p.block_size;
+      const int32_t off = slot - blk * p.block_size;
+      const int64_t dst_base = static_cast<int64_t>(blk) * p.blk_stride + static_cast<int64_t>(off) * p.slot_stride;
+#pragma unroll
+      for (int u = 0; u < CPL; ++u) store16_nt(p.k_cache + dst_base + dofs[u], kb[q][u]);
+#pragma unroll
+      for (int u = 0; u < CPL; ++u) store16_nt(p.v_cache + dst_base + dofs[u], vb[q][u]);
+    }
     j0 += 64 * CPL;
   } while (j0 < cpt);
 }
@@ -142,7 +158,7 @@ extern "C" int kvp_append_bf16(const void* key, int64_t key_tok_stride, int64_t 
   p.num_kv_heads = num_kv_heads;
   p.block_size = block_size;
 
-  const dim3 grid((num_tokens + kAppendWaves - 1) / kAppendWaves);
+  const dim3 grid((num_tokens + kAppendTokensPerGroup - 1) / kAppendTokensPerGroup);
   const dim3 block(64 * kAppendWaves);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int cpt = num_kv_heads * (head_dim / 8);

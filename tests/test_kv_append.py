@@ -168,3 +168,21 @@ def test_append_golden(cuda_device):
     _store(key, value, kc, vc, torch.from_numpy(f["slot_mapping"]).to(cuda_device))
     torch.cuda.synchronize()
     assert np.array_equal(pool.cpu().numpy(), f["pool_after"])
+
+
+@pytest.mark.parametrize("n,hkv,d", [(1, 8, 128), (3, 8, 128), (13, 2, 64), (9, 16, 256), (5, 12, 128)])
+def test_append_ragged_counts_and_long_rows(cuda_device, n, hkv, d):
+    """Token counts that leave a wave with one token and a workgroup partly empty, and
+    rows longer than one pass of the wave (16 x 256 bf16 = 512 chunks per row)."""
+    g = gen(3000 + n * hkv + d)
+    nb, bs = 6, 64
+    key, value = randn_bf16((n, hkv, d), g), randn_bf16((n, hkv, d), g)
+    kc, vc = randn_bf16((nb, bs, hkv, d), g), randn_bf16((nb, bs, hkv, d), g)
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(torch.int32)
+    if n > 2:
+        slots[n // 2] = -1
+    want_k, want_v = _oracle_append(key, value, kc, vc, slots)
+    dk, dv = kc.to(cuda_device), vc.to(cuda_device)
+    _store(key.to(cuda_device), value.to(cuda_device), dk, dv, slots.to(cuda_device))
+    torch.cuda.synchronize()
+    assert bits_equal(dk.cpu(), want_k) and bits_equal(dv.cpu(), want_v)
