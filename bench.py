@@ -863,6 +863,125 @@ def bench_e2e(num_seqs: int = 256):
     return res
 
 
+# ------------------------------------------------------------------ reference-design run
+
+_EAGER_LEN: dict = {}
+
+
+def _eager_attention_forward(self, positions: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
+    """Qwen3Attention.forward with the paged KV path in plain PyTorch ops, the comparator
+    standing in for the reference's design on this GPU: q/k RMSNorm and RoPE as separate
+    steps, the append as an index-put into the pages, and attention as gather-then-softmax
+    over the pages with explicit masks (bottom-right causal in prefill).  bf16 products
+    take contiguous operands; scores and softmax are fp32.  Harness only: the product
+    path never uses it."""
+    import torch.nn.functional as F
+
+    from kavor_amd.layers import fused
+    from kavor_amd.utils.context import get_context
+
+    T, Dh = hidden.shape[0], self.head_dim
+    Hq, Hkv = self.num_heads, self.num_kv_heads
+    G = Hq // Hkv
+    qkv = F.linear(hidden, self.qkv_proj)
+    q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+    q = fused.rms_norm(q.reshape(T, Hq, Dh), self.q_norm.weight, self.q_norm.eps)
+    k = fused.rms_norm(k.reshape(T, Hkv, Dh), self.k_norm.weight, self.k_norm.eps)
+    v = v.reshape(T, Hkv, Dh)
+    cs = self.rope[positions.long()]
+    cos, sin = cs[:, None, :Dh // 2], cs[:, None, Dh // 2:]
+
+    def rope(x):
+        x1, x2 = x.float().chunk(2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(torch.bfloat16)
+
+    q, k = rope(q), rope(k)
+    ctx = get_context()
+    kc, vc = self.attn.k_cache[0], self.attn.v_cache[0]
+    nb, bs = kc.shape[0], kc.shape[1]
+    if kc.numel() > 0 and ctx.slot_mapping is not None:  # eager steps carry no padding slots
+        sl = ctx.slot_mapping.long()
+        kc[sl // bs, sl % bs] = k
+        vc[sl // bs, sl % bs] = v
+    scale = Dh ** -0.5
+    if ctx.is_prefill:
+        out = torch.empty(T, Hq, Dh, dtype=torch.bfloat16, device=q.device)
+        cq, ck = ctx.cu_seqlens_q.tolist(), ctx.cu_seqlens_k.tolist()
+        for i in range(len(cq) - 1):
+            qlen, klen = cq[i + 1] - cq[i], ck[i + 1] - ck[i]
+            if ctx.block_tables is not None:
+                blocks = ctx.block_tables[i, :-(-klen // bs)].long()
+                ks, vs = kc[blocks].reshape(-1, Hkv, Dh)[:klen], vc[blocks].reshape(-1, Hkv, Dh)[:klen]
+            else:
+                ks, vs = k[ck[i]:ck[i + 1]], v[ck[i]:ck[i + 1]]
+            qh = q[cq[i]:cq[i + 1]].transpose(0, 1).float().contiguous()                     # [Hq, n, D]
+            kt = ks.repeat_interleave(G, dim=1).permute(1, 2, 0).float().contiguous()       # [Hq, D, k]
+            vh = vs.repeat_interleave(G, dim=1).transpose(0, 1).float().contiguous()        # [Hq, k, D]
+            sc = torch.matmul(qh, kt) * scale
+            r = torch.arange(qlen, device=q.device)[:, None]
+            c = torch.arange(klen, device=q.device)[None, :]
+            sc = sc.masked_fill(c > r + (klen - qlen), float("-inf"))
+            out[cq[i]:cq[i + 1]] = torch.matmul(torch.softmax(sc, dim=-1), vh).transpose(0, 1).to(torch.bfloat16)
+    else:
+        # One host read per step, shared by the layers: the runner publishes a new Context
+        # per step, and holding it keeps its identity from being reused.
+        if _EAGER_LEN.get("ctx") is not ctx:
+            _EAGER_LEN["ctx"] = ctx
+            _EAGER_LEN["len"] = int(ctx.context_lens.max())
+        W = -(-_EAGER_LEN["len"] // bs)
+        L = W * bs
+        bt = ctx.block_tables[:, :W].long().clamp(0, nb - 1)
+        kt = kc[bt].reshape(T, L, Hkv, Dh).permute(0, 2, 3, 1).contiguous()   # [B, Hkv, D, L]
+        vg = vc[bt].reshape(T, L, Hkv, Dh).transpose(1, 2).contiguous()        # [B, Hkv, L, D]
+        sc = torch.matmul(q.reshape(T, Hkv, G, Dh), kt).float() * scale       # [B, Hkv, G, L]
+        pad = torch.arange(L, device=q.device)[None, :] >= ctx.context_lens[:, None]
+        sc = sc.masked_fill(pad[:, None, None, :], float("-inf"))
+        # Positions past a sequence's length hold whatever the pages held (NaN bit
+        # patterns included): a zero softmax weight times NaN is NaN, so clear them.
+        vg.masked_fill_(pad[:, None, :, None], 0)
+        out = torch.matmul(torch.softmax(sc, dim=-1).to(torch.bfloat16), vg).reshape(T, Hq, Dh)
+    return F.linear(out.reshape(T, Hq * Dh), self.o_proj)
+
+
+def bench_e2e_window(max_new: int = 32):
+    """Decode throughput of the engine against the same engine with the PyTorch-eager
+    attention path (the reference-design comparator), both eager (no graphs: the
+    comparator's shapes change every step), on the end-to-end prompts with every
+    request's output capped at `max_new` tokens."""
+    from kavor_amd.engine import qwen3
+    from kavor_amd.engine.llm_engine import LLM
+    from kavor_amd.sampling_params import SamplingParams
+
+    prompts, _ = e2e_workload()
+    sps = SamplingParams(temperature=0.0, ignore_eos=True, max_tokens=max_new)
+    res = {}
+    native = qwen3.Qwen3Attention.forward
+    for name, fwd in (("hip_path", native), ("torch_eager_attention", _eager_attention_forward)):
+        qwen3.Qwen3Attention.forward = fwd
+        try:
+            llm = LLM(None, enforce_eager=True, max_model_len=4096, seed=0)
+            llm.generate([prompts[0][:16]], SamplingParams(temperature=0.0, max_tokens=4, ignore_eos=True))
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            llm.generate(prompts, sps)
+            wall = time.perf_counter() - t
+            sm = llm.throughput_summary()
+            res[name] = dict(output_tok_s=round(len(prompts) * max_new / wall, 1),
+                             decode_tok_s=round(sm["decode_tok_s"], 1), wall_s=round(wall, 3))
+            llm.exit()
+            del llm
+        finally:
+            qwen3.Qwen3Attention.forward = native
+            _EAGER_LEN.clear()
+        torch.cuda.empty_cache()
+        print(f"e2e window {name}: {res[name]['decode_tok_s']} decode tok/s", file=sys.stderr, flush=True)
+    res["decode_speedup"] = round(res["hip_path"]["decode_tok_s"] / res["torch_eager_attention"]["decode_tok_s"], 2)
+    res["workload"] = (f"the 256 end-to-end prompts, {max_new} greedy output tokens each, both engines eager "
+                       "(no graphs); comparator: q/k norm and RoPE as separate steps, index-put append, "
+                       "gather + fp32 softmax attention in PyTorch")
+    return res
+
+
 # ----------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -932,6 +1051,7 @@ def main() -> int:
         del inp
         torch.cuda.empty_cache()
         extras["e2e_qwen3_0.6b"] = bench_e2e(args.e2e_seqs)
+        extras["e2e_qwen3_0.6b"]["reference_design"] = bench_e2e_window()
         if not args.no_cpu_baseline:
             extras["e2e_qwen3_0.6b"]["cpu_baseline"] = cpu_baseline_e2e()
 

@@ -106,3 +106,25 @@ def test_sampling_with_temperature_runs_and_eos_stops(graph_llm):
         if len(toks) < 32:
             assert toks[-1] == TINY.eos_token_id
     torch.cuda.synchronize()
+
+
+def test_reference_design_comparator_is_correct(cuda_device, monkeypatch):
+    """The benchmark's reference-design comparator (PyTorch-eager append and attention in
+    place of the HIP path) generates reference-correct tokens too, with prefix-cache hits
+    and chunked prefill in the mix, so the throughput comparison is between two correct
+    engines."""
+    import bench
+    from kavor_amd.engine import qwen3
+
+    monkeypatch.setattr(qwen3.Qwen3Attention, "forward", bench._eager_attention_forward)
+    llm = LLM(TINY, kvcache_block_size=64, max_model_len=1024, num_kvcache_blocks=64,
+              max_num_seqs=8, max_num_batched_tokens=256, enforce_eager=True, seed=0)
+    try:
+        base = _prompts(9, [150])[0]
+        prompts = [base, base + [7, 8], _prompts(10, [300])[0], [3]]
+        sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True) for m in (20, 9, 12, 30)]
+        outs = llm.generate(prompts, sps)
+        assert [len(o["token_ids"]) for o in outs] == [sp.max_tokens for sp in sps]
+        _check(llm, prompts, outs)
+    finally:
+        llm.exit()
