@@ -13,7 +13,10 @@
 //   waves = 4 kv heads; ceil(Hkv / 4) consecutive workgroups form a group that walks
 //   one contiguous range of steps for all kv heads (kv heads of one token row share HBM
 //   pages and are fetched together).  Every group gets the same number of steps
-//   (exact balance whatever the context lengths), at least 16 steps (256 tokens).
+//   (exact balance whatever the context lengths), and at least 128 tokens: a large batch
+//   is split by the grid (the range limit does not bind), while a small one is cut into
+//   short ranges so that it still spreads over many CUs (measured with 8 sequences of
+//   500-2000 tokens: 34.6 us per call with 512-token ranges, 19.5 us with 128).
 //   A wave owns all G = Hq / Hkv query heads of its kv head, so GQA costs no extra KV
 //   traffic.  Lane (r = lane/16, c = lane%16) owns dims [8c, 8c+8) of tokens 4i+r of a
 //   step (i = 0..3): 4 dwordx4 loads of K and 4 of V per lane, each 16-lane row
@@ -45,7 +48,7 @@ namespace kvp {
 constexpr int kDecodeHeadDim = 128;
 constexpr int kDecodeWaves = 4;  // kv heads per workgroup
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
-constexpr int kMinRangeTokens = 512;        // a range covers at least 512 tokens
+constexpr int kMinRangeTokens = 128;        // a range covers at least 128 tokens
 constexpr int kMinStepTokens = 16;           // smallest step (G = 8); G <= 4 steps 32 tokens
 constexpr int kMaxSeqsPerLaunch = 4096;      // size of the LDS prefix-sum table
 constexpr int kHeaderInts = 16;              // workspace header before the prefix table
@@ -71,8 +74,8 @@ struct DecodeParams {
   uint16_t* out;
   int64_t o_seq_stride, o_head_stride;
   int32_t* header;  // [0] steps per range, [kHeaderInts ..] step prefix sums (B + 1)
-  float* part_o;    // [num_seqs][num_q_heads][max_parts][128]
-  float* part_ml;   // [num_seqs][num_q_heads][max_parts][2] = (max, sum)
+  float* part_o;    // [max_parts][num_seqs][num_q_heads][128]: part-major, so the parts in use
+  float* part_ml;   // [max_parts][num_seqs][num_q_heads][2] = (max, sum)   stay compact
 };
 
 __device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
@@ -273,7 +276,7 @@ __device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh
         o.w = pack_bf16x2(a[6] * inv, a[7] * inv);
         *reinterpret_cast<uint4*>(p.out + b * p.o_seq_stride + h * p.o_head_stride + 8 * c) = o;
       } else {
-        const int64_t row = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.max_parts + part;
+        const int64_t row = (static_cast<int64_t>(part) * p.num_seqs + b) * p.num_q_heads + h;
         float4* dst = reinterpret_cast<float4*>(p.part_o + row * kDecodeHeadDim + 8 * c);
         dst[0] = make_float4(a[0], a[1], a[2], a[3]);
         dst[1] = make_float4(a[4], a[5], a[6], a[7]);
@@ -404,7 +407,8 @@ __global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_ker
   const int b = blockIdx.y;
   const int d = threadIdx.x % D;
   if (h >= p.num_q_heads) return;
-  const int64_t row0 = (static_cast<int64_t>(b) * p.num_q_heads + h) * p.max_parts;
+  const int64_t row0 = static_cast<int64_t>(b) * p.num_q_heads + h;
+  const int64_t part_rows = static_cast<int64_t>(p.num_seqs) * p.num_q_heads;  // rows between parts
   const float* ml = p.part_ml + row0 * 2;
   const float* po = p.part_o + row0 * D + d;
   float2 st0[kSpecParts];
@@ -412,8 +416,8 @@ __global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_ker
 #pragma unroll
   for (int k = 0; k < kSpecParts; ++k) {
     const int s = min(k, p.max_parts - 1);
-    st0[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
-    ov0[k] = po[static_cast<int64_t>(s) * D];
+    st0[k] = *reinterpret_cast<const float2*>(ml + 2 * s * part_rows);
+    ov0[k] = po[s * part_rows * D];
   }
   const int cb = p.header[kHeaderInts + b], cb1 = p.header[kHeaderInts + b + 1];
   const int spr = p.header[0];
@@ -445,8 +449,8 @@ __global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_ker
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int s = min(s0 + k, np - 1);
-      st[k] = *reinterpret_cast<const float2*>(ml + 2 * s);
-      ov[k] = po[static_cast<int64_t>(s) * D];
+      st[k] = *reinterpret_cast<const float2*>(ml + 2 * s * part_rows);
+      ov[k] = po[s * part_rows * D];
     }
     float bm = mm;
 #pragma unroll

@@ -78,9 +78,9 @@ def test_decode_rejects_bad_arguments_on_host():
 
 def test_decode_workspace_size_formula():
     # 256-byte-aligned header (16 ints + a 4097-entry prefix table), then per (sequence,
-    # query head) up to ceil(max_tokens / 512) + 1 partial states of 130 floats
+    # query head) up to ceil(max_tokens / 128) + 1 partial states of 130 floats
     header = ((16 + 4097) * 4 + 255) // 256 * 256
-    parts = -(-(16 * 256) // 512) + 1
+    parts = -(-(16 * 256) // 128) + 1
     assert _lib.lib().kvp_decode_workspace_bytes(512, 16, 128, 16, 256) == header + 512 * 16 * parts * 130 * 4
     assert _lib.lib().kvp_decode_workspace_bytes(9000, 16, 128, 16, 256) == header + 4096 * 16 * parts * 130 * 4
     assert _lib.lib().kvp_decode_workspace_bytes(0, 16, 128, 16, 256) == 0
