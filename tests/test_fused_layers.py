@@ -59,8 +59,11 @@ def _pool(num_blocks, bs, hkv, D, dev, gen):
     return raw, pool, page_views(pool, bs, hkv, D)
 
 
-@pytest.mark.parametrize("T,hq,hkv", [(64, 32, 8), (300, 16, 8), (5, 16, 16)])
+@pytest.mark.parametrize("T,hq,hkv", [(64, 32, 8), (300, 16, 8), (5, 16, 16), (1, 16, 8),
+                                      (2048, 16, 8), (2050, 32, 8)])
 def test_qk_norm_rope_append(cuda_device, T, hq, hkv):
+    """Below 2048 tokens each wave takes one head row per 16-lane row; from 2048 on, eight
+    (one wave per token for 32 rows; with 32 q + 8 + 8 rows, a second, half-empty group)."""
     D, bs, nb, max_pos = 128, 64, 40, 4096
     g = torch.Generator().manual_seed(2)
     qkv = _randn(T, (hq + 2 * hkv) * D, gen=g)
