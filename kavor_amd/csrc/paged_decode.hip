@@ -36,7 +36,6 @@
 //   traffic is about 2 states per group per sequence boundary: well under 1% of the KV
 //   bytes.
 #include <math.h>
-#include <stdlib.h>
 
 #include <algorithm>
 #include <atomic>
@@ -506,12 +505,8 @@ static int resident_workgroups() {
 
 template <int G, int STEP>
 static void launch_decode(DecodeParams p, int64_t max_tokens, hipStream_t s) {
-  static const int forced = [] {
-    const char* env = getenv("KVP_DECODE_GRID");
-    return env ? atoi(env) : 0;
-  }();
   const int64_t groups_per_range = (p.num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
-  const int64_t grid0 = forced > 0 ? forced : resident_workgroups<G, STEP>();
+  const int64_t grid0 = resident_workgroups<G, STEP>();
   // no more ranges than minimum-size ranges over the largest possible work
   const int64_t max_ranges = std::max<int64_t>(1, (max_tokens + kMinRangeTokens - 1) / kMinRangeTokens);
   p.step_tokens = STEP;
