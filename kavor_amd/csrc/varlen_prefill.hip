@@ -22,9 +22,13 @@
 //   (v_permlane32_swap, no LDS) and P feeds the second MFMA straight from registers.  The
 //   softmax scale is folded into the exponent (exp2(fma(s, scale*log2 e, -m))).
 //   Q stays in registers for the whole key loop (8 x 16 bytes per lane).
-//   The 1-D grid runs the longest (last) query tiles of every sequence and kv head
-//   first, then the shorter ones; pairs of neighbouring query tiles share an XCD.
+//   Work order: every workgroup ranks the units of work (a pair of neighbouring query
+//   tiles of one sequence and kv head) by cost and takes the one of its own rank, so
+//   the most expensive units start first and the cheap ones fill in behind them; the
+//   two tiles of a unit run on one XCD.
 #include <math.h>
+
+#include <algorithm>
 
 #include "common.h"
 
@@ -40,6 +44,11 @@ constexpr int kKeyTile = 64;
 constexpr int kKStride = kPrefillHeadDim + 8;  // LDS row pitch of the K tile (bf16)
 constexpr int kXcdGroup = 2;  // neighbouring query tiles of one (sequence, kv head) per XCD
 constexpr int kVStride = kPrefillHeadDim + 32;  // LDS row pitch of the V tile (bf16): 80 dwords keeps the transposed reads conflict-free
+// Sequences per launch: their lengths and starts (8 bytes each) are staged in the idle
+// K and V tile buffers before the first tile; larger batches run as consecutive launches.
+constexpr int kMaxPrefillSeqs = 4096;
+static_assert(2 * kKeyTile * kKStride * 2 >= kMaxPrefillSeqs * 8, "lengths must fit the K buffers");
+static_assert(2 * kKeyTile * kVStride * 2 >= kMaxPrefillSeqs * 8, "starts must fit the V buffers");
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -58,9 +67,9 @@ struct PrefillParams {
   int32_t max_blocks;
   const int32_t* cu_q;
   const int32_t* cu_k;
-  int32_t num_tiles;  // query tiles per (sequence, kv head) covered by the grid
+  int32_t num_seqs;
+  int32_t pair_slots;
   int32_t num_kv_heads;
-  int32_t total_work;
   float scale_log2;
   uint16_t* out;
   int64_t o_tok_stride, o_head_stride;
@@ -101,49 +110,139 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   constexpr int D = kPrefillHeadDim;
   constexpr int TOK = kPrefillRows / G;  // query tokens per tile
 
-  // Work order: rounds of GRP tile slots (slot 0 = the last, longest query tile of a
-  // sequence), then sequence, then kv head, then the GRP slots of the round.  Long tiles
-  // start first and the short ones fill in behind them (0.82 -> 0.58 ms on the
-  // prefix-cached 32-sequence workload against (sequence, kv head, tile) order dealt to
-  // the XCDs in contiguous chunks).  The hardware deals workgroup ids round-robin to the
-  // 8 XCDs, so ids b and b + 8 share an XCD: the GRP neighbouring query tiles of one
-  // (sequence, kv head), which read nearly the same K/V, get such ids and run together
-  // on one XCD, sharing its L2 (0.53 -> 0.50 ms).
-  constexpr int GRP = kXcdGroup;
+  // Work order.  A unit is a pair of neighbouring query tiles of one (sequence, kv
+  // head); its cost is the key-tile count of its longer (later) tile.  Workgroup pair
+  // (b, b + 8) takes the unit of rank m in decreasing cost: the hardware deals
+  // workgroup ids round-robin to the 8 XCDs, so the two tiles, which read nearly the
+  // same K/V, run together on one XCD and share its L2 (0.53 -> 0.50 ms on the
+  // prefix-cached 32-sequence workload).  The most expensive units start first and the
+  // cheap ones fill in behind them: 0.82 -> 0.58 ms for "last tiles first" against
+  // (sequence, kv head, tile) order, and 0.457 -> 0.437 ms for the global cost order
+  // against "last tiles first".  The rank is found by a binary search over cost levels
+  // on closed-form unit counts per sequence (no sort, no workspace).
   const int b = blockIdx.x;
-  const int m = (b / (8 * GRP)) * 8 + (b % 8);   // group index; its GRP items share XCD b % 8
-  const int work = m * GRP + (b % (8 * GRP)) / 8;
-  if (work >= p.total_work) return;
-  const int nseq = p.total_work / (p.num_tiles * p.num_kv_heads);
-  const int per_round = nseq * p.num_kv_heads * GRP;
-  const int rem = work % per_round;
-  const int tile_slot = (work / per_round) * GRP + rem % GRP;
-  const int kvh = (rem / GRP) % p.num_kv_heads;
-  const int s = rem / (GRP * p.num_kv_heads);
-
+  const int m0 = (b / (8 * kXcdGroup)) * 8 + (b % 8);  // this workgroup pair's rank
+  const int member = (b % (8 * kXcdGroup)) / 8;        // which tile of the unit
+  const int nseq = p.num_seqs;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int n = lane & 31;   // this lane's query row within the wave
   const int hf = lane >> 5;  // which half of the MFMA K-dim this lane feeds
 
-  const int q_start = p.cu_q[s];
-  const int qlen = p.cu_q[s + 1] - q_start;
-  const int k_start = p.cu_k[s];
-  const int klen = p.cu_k[s + 1] - k_start;
-  const int diag = klen - qlen;  // bottom-right causal offset
-
-  bool bad = false;
-  if (PAGED && klen > p.max_blocks * p.block_size) bad = true;
-
   // Two buffers of the K and V tiles (row-major, padded rows): tile i+1 is written while
   // other waves may still read tile i.
   __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKeyTile * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kKeyTile * kVStride];
   __shared__ int s_bad;
+  // Before the first K/V tile is staged, the K buffers hold every sequence's
+  // (query length, key length) and the V buffers its (query start, key start).
+  int2* s_len = reinterpret_cast<int2*>(&s_k[0][0]);
+  int2* s_start = reinterpret_cast<int2*>(&s_v[0][0]);
+  const int J = p.pair_slots;  // tile pairs per (sequence, kv head) the grid covers
 
+  // Units of sequence (ql, kl) whose first tile needs at least L key tiles.  Tile i of
+  // TOK query tokens needs ceil(min(kl, min(ql, (i+1) TOK) + kl - ql) / 64) key tiles,
+  // which grows with i; unit j (< J) starts with tiles ntl-1-2j and ntl-2-2j.
+  auto units_ge = [&](int ql, int kl, int L) -> int {
+    const int ntl = (ql + TOK - 1) / TOK;
+    if (ntl == 0) return 0;
+    const int all = min(J, (ntl + 1) / 2);
+    if (L <= 0) return all;
+    const int x = kKeyTile * (L - 1);
+    if (kl <= x) return 0;
+    if (!CAUSAL) return all;
+    const int y = x - (kl - ql);
+    const int fi = y <= 0 ? 0 : y / TOK;
+    return min(all, (ntl - 1 - fi) / 2 + 1);
+  };
+  auto wave_sum = [&](int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+  };
+  auto wave_max = [&](int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    return v;
+  };
+  auto count_ge = [&](int L) {
+    int c = 0;
+    for (int i = lane; i < nseq; i += 64) {
+      const int2 l = s_len[i];
+      c += units_ge(l.x, l.y, L);
+    }
+    return wave_sum(c) * p.num_kv_heads;
+  };
+
+  for (int i = tid; i < nseq; i += kPrefillThreads) {
+    const int q0s = p.cu_q[i], q1s = p.cu_q[i + 1], k0s = p.cu_k[i], k1s = p.cu_k[i + 1];
+    s_len[i] = make_int2(q1s - q0s, k1s - k0s);
+    s_start[i] = make_int2(q0s, k0s);
+  }
   if (tid == 0) s_bad = 0;  // sticky for the workgroup: one sequence, one block table
   __syncthreads();
+
+  // Rank r in the order of decreasing cost (ties: sequence, kv head, unit).  Every wave
+  // computes the same answer.
+  const int r = m0;
+  if (r >= count_ge(0)) return;  // uniform; no barrier follows
+  int kmax = 0;
+  for (int i = lane; i < nseq; i += 64) kmax = max(kmax, s_len[i].y);
+  int lo = 0, hi = (wave_max(kmax) + kKeyTile - 1) / kKeyTile + 1, c_hi = 0;
+  while (hi - lo > 1) {  // count_ge(lo) > r >= count_ge(hi) = c_hi
+    const int mid = (lo + hi) >> 1;
+    const int c = count_ge(mid);
+    if (c > r) lo = mid;
+    else { hi = mid; c_hi = c; }
+  }
+  int rr = r - c_hi;  // rank among the units of cost level lo
+  int s = -1, e_s = 1, skip = 0;
+  for (int base = 0; base < nseq; base += 64) {
+    const int i = base + lane;
+    int e = 0, ghi = 0;
+    if (i < nseq) {
+      const int2 l = s_len[i];
+      ghi = units_ge(l.x, l.y, lo + 1);
+      e = (units_ge(l.x, l.y, lo) - ghi) * p.num_kv_heads;
+    }
+    int incl = e;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
+    }
+    const int tot = __shfl(incl, 63);
+    if (rr < tot) {
+      const unsigned long long hit = __ballot(incl > rr);
+      const int w = __builtin_ctzll(hit);
+      s = base + w;
+      e_s = __shfl(e, w);
+      skip = __shfl(ghi, w);
+      rr -= __shfl(incl - e, w);
+      break;
+    }
+    rr -= tot;
+  }
+  if (s < 0) return;  // unreachable while the counts agree (uniform)
+  // Every lane holds the same values: readfirstlane keeps them (and the addresses
+  // derived from them) in scalar registers.
+  s = __builtin_amdgcn_readfirstlane(s);
+  const int per_head = __builtin_amdgcn_readfirstlane(e_s) / p.num_kv_heads;
+  rr = __builtin_amdgcn_readfirstlane(rr);
+  const int kvh = rr / per_head;
+  const int jj = __builtin_amdgcn_readfirstlane(skip) + rr % per_head;
+  const int2 ls = s_len[s];
+  const int2 st = s_start[s];
+  const int q_start = __builtin_amdgcn_readfirstlane(st.x);
+  const int qlen = __builtin_amdgcn_readfirstlane(ls.x);
+  const int k_start = __builtin_amdgcn_readfirstlane(st.y);
+  const int klen = __builtin_amdgcn_readfirstlane(ls.y);
+  const int diag = klen - qlen;  // bottom-right causal offset
+  __syncthreads();  // every wave has read the lengths: the buffers may be staged
+
+  bool bad = false;
+  if (PAGED && klen > p.max_blocks * p.block_size) bad = true;
 
   // The first 64 block-table entries of the sequence, one per lane, read with readlane:
   // a tile's block id then costs no memory round trip on the way to its K/V loads.
@@ -203,7 +302,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   const int ntiles_seq = (qlen + TOK - 1) / TOK;
   // Grid-stride over query tiles (a sequence longer than the grid's max_seqlen_q is
   // still covered); the last (longest) tiles go first.
-  for (int t = tile_slot; t < ntiles_seq; t += p.num_tiles) {
+  for (int t = 2 * jj + member; t < ntiles_seq; t += 2 * J) {
     const int tile = ntiles_seq - 1 - t;
     const int q0 = tile * TOK;
 
@@ -443,9 +542,9 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
 
   const int tok_per_tile = kPrefillRows / G;
   const int64_t num_tiles = (static_cast<int64_t>(max_seqlen_q) + tok_per_tile - 1) / tok_per_tile;
-  const int64_t num_tiles_pad = (num_tiles + kXcdGroup - 1) / kXcdGroup * kXcdGroup;
-  const int64_t total = num_tiles_pad * num_kv_heads * num_seqs;
-  if (total > (1ll << 30)) return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: grid too large");
+  const int64_t pair_slots = (num_tiles + kXcdGroup - 1) / kXcdGroup;
+  if (pair_slots * num_kv_heads * kMaxPrefillSeqs * kXcdGroup > (1ll << 30))
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: grid too large");
 
   PrefillParams p;
   p.q = static_cast<const uint16_t*>(q);
@@ -459,30 +558,38 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
   p.v_blk_stride = v_block_stride;
   p.v_tok_stride = v_tok_stride;
   p.v_head_stride = v_head_stride;
-  p.block_tables = block_tables;
   p.bt_stride = block_table_stride;
   p.num_cache_blocks = num_cache_blocks;
   p.block_size = paged ? block_size : kKeyTile;
   p.max_blocks = max_blocks_per_seq;
-  p.cu_q = cu_seqlens_q;
-  p.cu_k = cu_seqlens_k;
-  p.num_tiles = static_cast<int32_t>(num_tiles_pad);
+  p.pair_slots = static_cast<int32_t>(pair_slots);
   p.num_kv_heads = num_kv_heads;
-  p.total_work = static_cast<int32_t>(total);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
   p.out = static_cast<uint16_t*>(out);
   p.o_tok_stride = out_tok_stride;
   p.o_head_stride = out_head_stride;
 
   constexpr int64_t kRound = 8 * kXcdGroup;  // one group on each of the 8 XCDs
-  const dim3 grid(static_cast<unsigned>((total + kRound - 1) / kRound * kRound));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool c = causal != 0;
-  switch (G) {
-    case 1: launch_prefill<1>(paged, c, grid, s, p); break;
-    case 2: launch_prefill<2>(paged, c, grid, s, p); break;
-    case 4: launch_prefill<4>(paged, c, grid, s, p); break;
-    default: launch_prefill<8>(paged, c, grid, s, p); break;
+  // cu_seqlens hold absolute offsets, so a launch over sequences [s0, s0 + n) reads
+  // the same q/k/out rows through the offset pointers.
+  for (int s0 = 0; s0 < num_seqs; s0 += kMaxPrefillSeqs) {
+    const int n = std::min(kMaxPrefillSeqs, num_seqs - s0);
+    p.cu_q = cu_seqlens_q + s0;
+    p.cu_k = cu_seqlens_k + s0;
+    p.block_tables = paged ? block_tables + s0 * block_table_stride : nullptr;
+    p.num_seqs = n;
+    const int64_t total = pair_slots * num_kv_heads * n * kXcdGroup;
+    const dim3 grid(static_cast<unsigned>((total + kRound - 1) / kRound * kRound));
+    switch (G) {
+      case 1: launch_prefill<1>(paged, c, grid, s, p); break;
+      case 2: launch_prefill<2>(paged, c, grid, s, p); break;
+      case 4: launch_prefill<4>(paged, c, grid, s, p); break;
+      default: launch_prefill<8>(paged, c, grid, s, p); break;
+    }
+    const int rc = launch_status("kvp_varlen_prefill_bf16");
+    if (rc != KVP_OK) return rc;
   }
-  return launch_status("kvp_varlen_prefill_bf16");
+  return KVP_OK;
 }

@@ -246,3 +246,32 @@ def test_paged_relocated_pages_are_bitwise_identical(cuda_device):
     a = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d)).cpu()
     b = _prefill(q.to(d), k2.to(d), v2.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt2.to(d)).cpu()
     assert bits_equal(a, b)
+
+
+@pytest.mark.parametrize("paged", [True, False])
+def test_more_sequences_than_one_launch(cuda_device, paged):
+    """4100 sequences run as two launches (4096 + 4): the second reads its cu_seqlens and
+    block-table rows through offset pointers and writes the same absolute rows."""
+    g = gen(260 + paged)
+    nseq, bs, nb = 4100, 64, 64
+    qlens = [int(x) for x in torch.randint(1, 4, (nseq,), generator=g)]
+    prefix = [int(x) for x in torch.tensor([0, 5, 64])[torch.randint(0, 3, (nseq,), generator=g)]]
+    if not paged:
+        prefix = [0] * nseq
+    klens = [a + b for a, b in zip(qlens, prefix)]
+    q = randn_bf16((sum(qlens), 4, 128), g)
+    d = cuda_device
+    if paged:
+        kc, vc = contiguous_caches(nb, bs, 2, 128, g)
+        # pages shared between sequences (as prefix-cache hits share them), -1 past the need
+        bt = torch.randint(0, nb, (nseq, 2), generator=g, dtype=torch.int32)
+        bt[torch.tensor([math.ceil(k / bs) for k in klens]) == 1, 1] = -1
+        out = _prefill(q.to(d), kc.to(d), vc.to(d), _cu(qlens).to(d), _cu(klens).to(d), 3, bt=bt.to(d))
+        want = ref.varlen_prefill(q, kc, vc, _cu(qlens), _cu(klens), SCALE, block_tables=bt)
+    else:
+        k = randn_bf16((sum(klens), 2, 128), g)
+        v = randn_bf16((sum(klens), 2, 128), g)
+        out = _prefill(q.to(d), k.to(d), v.to(d), _cu(qlens).to(d), _cu(klens).to(d), 3)
+        want = ref.varlen_prefill(q, k, v, _cu(qlens), _cu(klens), SCALE)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
