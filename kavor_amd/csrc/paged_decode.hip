@@ -81,6 +81,15 @@ __device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
   return *reinterpret_cast<const uint4*>(ptr);
 }
 
+// A wave-uniform read of read-only metadata (context lengths, block tables) through the
+// constant address space, so it compiles to a scalar load.  Scalar loads are counted
+// apart from the vector loads of the K/V stream: waiting for a block id does not wait
+// for the KV loads in flight (as a vector load's wait would, vector loads complete in
+// order), and a block id loaded one block ahead is waited for only where it is used.
+__device__ __forceinline__ int load_uniform(const int32_t* base, int64_t idx) {
+  return ((const __attribute__((address_space(4))) int32_t*)(base))[idx];
+}
+
 // Steps of a sequence; 0 for empty or impossible contexts (written separately).
 __device__ __forceinline__ int seq_steps(int ctx, const DecodeParams& p) {
   if (ctx <= 0 || ctx > p.max_blocks * p.block_size) return 0;
@@ -154,7 +163,7 @@ struct StepCursor {
 __device__ __forceinline__ void cursor_start_seq(const DecodeParams& p, StepCursor& cur, int b, int j) {
   cur.b = b;
   cur.j = j;
-  cur.ctx = p.context_lens[b];
+  cur.ctx = load_uniform(p.context_lens, b);
   cur.nsteps = seq_steps(cur.ctx, p);
   cur.lblk = -1;
   cur.blk = 0;
@@ -173,14 +182,14 @@ __device__ __forceinline__ int64_t step_base(const DecodeParams& p, StepCursor& 
   const int lblk = t0 / p.block_size;
   if (lblk != cur.lblk) {
     const int32_t* row = p.block_tables + cur.b * p.bt_stride;
-    int blk = (cur.lblk >= 0 && lblk == cur.lblk + 1 && cur.pf_blk != -1) ? cur.pf_blk : row[lblk];
+    int blk = (cur.lblk >= 0 && lblk == cur.lblk + 1 && cur.pf_blk != -1) ? cur.pf_blk : load_uniform(row, lblk);
     if (blk < 0 || blk >= p.num_cache_blocks) {
       cur.bad = true;
       blk = 0;
     }
     cur.blk = blk;
     cur.lblk = lblk;
-    cur.pf_blk = (lblk + 1) * p.block_size < cur.ctx ? row[lblk + 1] : -1;
+    cur.pf_blk = (lblk + 1) * p.block_size < cur.ctx ? load_uniform(row, lblk + 1) : -1;
   }
   nvalid = min(STEP, cur.ctx - t0);
   return static_cast<int64_t>(cur.blk) * p.blk_stride +
@@ -323,7 +332,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     else hi = mid;
   }
   StepCursor cur;
-  cursor_start_seq(p, cur, lo, S0 - s_cum[lo]);
+  lo = __builtin_amdgcn_readfirstlane(lo);  // uniform: the cursor's loads stay scalar
+  cursor_start_seq(p, cur, lo, __builtin_amdgcn_readfirstlane(S0 - s_cum[lo]));
   const int64_t head_off = static_cast<int64_t>(kvh) * p.head_stride + 8 * c;
 
   uint4 qv[G];
@@ -356,6 +366,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
         // next non-empty sequence: the one whose steps start at S + 1
         int nb = cur.b + 1;
         while (s_cum[nb + 1] == S + 1) ++nb;
+        nb = __builtin_amdgcn_readfirstlane(nb);
         cursor_start_seq(p, nxt, nb, 0);
 #pragma unroll
         for (int g = 0; g < G; ++g)
