@@ -292,11 +292,21 @@ __device__ __forceinline__ bool beats(float v, int i, float b, int j) {
   return v > b || (v == b && i < j);
 }
 
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);  // NaN-propagating (v_maximum3_f32)
+}
+
+// One workgroup per row.  Per chunk of 8 values a lane keeps, without branches, the
+// NaN-propagating maximum over its chunks, the chunk that first reached it and that
+// chunk's raw bits; the index inside the kept chunk is found once at the end.  A lane's
+// chunks come in increasing index order and only a strictly greater maximum (or a first
+// NaN) replaces the kept chunk, so ties keep the first occurrence.
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(ArgmaxParams p) {
   const uint16_t* row = p.logits + blockIdx.x * p.row_stride;
-  float best = -__builtin_inff();
-  int bi = 0x7fffffff;
   const int nvec = p.vocab >> 3;
+  float cmax = -__builtin_inff();
+  int bc = -1;
+  uint4 bw = make_uint4(0, 0, 0, 0);
   // kArgmaxBatch 16-byte loads per thread in flight before any is scanned; indices past
   // the row are clamped onto its last chunk and skipped.
   for (int c0 = threadIdx.x; c0 < nvec; c0 += kArgmaxThreads * kArgmaxBatch) {
@@ -307,13 +317,32 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(ArgmaxParams p) 
 #pragma unroll
     for (int u = 0; u < kArgmaxBatch; ++u) {
       const int c = c0 + u * kArgmaxThreads;
-      if (c >= nvec) break;
       float f[8];
       unpack8(w[u], f);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (beats(f[e], 8 * c + e, best, bi)) { best = f[e]; bi = 8 * c + e; }
+      const float m = max_nan(max_nan(max_nan(f[0], f[1]), max_nan(f[2], f[3])),
+                              max_nan(max_nan(f[4], f[5]), max_nan(f[6], f[7])));
+      const bool up = c < nvec && (bc < 0 || (m != m ? cmax == cmax : m > cmax));
+      cmax = up ? m : cmax;
+      bc = up ? c : bc;
+      bw.x = up ? w[u].x : bw.x;
+      bw.y = up ? w[u].y : bw.y;
+      bw.z = up ? w[u].z : bw.z;
+      bw.w = up ? w[u].w : bw.w;
     }
+  }
+  // The first value of the kept chunk equal to its maximum (for NaN: the first NaN);
+  // -0 and +0 compare equal, as in torch.argmax.
+  float best = -__builtin_inff();
+  int bi = 0x7fffffff;
+  if (bc >= 0) {
+    float f[8];
+    unpack8(bw, f);
+    int e0 = 7;
+#pragma unroll
+    for (int e = 7; e >= 0; --e)
+      if (f[e] == cmax || (cmax != cmax && f[e] != f[e])) e0 = e;
+    best = cmax;
+    bi = 8 * bc + e0;
   }
   const int tail = p.vocab - 8 * nvec;
   if (static_cast<int>(threadIdx.x) < tail) {

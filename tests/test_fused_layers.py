@@ -139,3 +139,36 @@ def test_greedy_argmax_odd_vocab_and_nan(cuda_device):
     buf[:, :1003] = logits                             # row stride 1008, vocab 1003
     got = greedy_argmax(buf.to(cuda_device)[:, :1003]).cpu()
     assert got.tolist() == [1001, 17, int(logits[2].float().argmax())]
+
+
+def test_greedy_argmax_screen_edge_cases(cuda_device):
+    """Rows that the per-chunk screen (max tree + NaN-probing sum) must hand to the exact
+    comparison: all -inf, signed zeros tied, +inf and -inf in one chunk, a negative NaN,
+    NaN after +inf; and a vocabulary that needs a second round of loads."""
+    V = 200_000  # 25,000 chunks: past one round of 1024 threads x 20 loads
+    rows = torch.full((8, V), -1.0).to(torch.bfloat16)
+    rows[0, :] = float("-inf")                               # all -inf: index 0
+    rows[1, 3], rows[1, 5] = -0.0, 0.0                       # -0 == +0: first index
+    rows[2, 3], rows[2, 5] = 0.0, -0.0
+    rows[3, 8], rows[3, 9], rows[3, 77_777] = float("inf"), float("-inf"), 5.0   # +inf wins
+    rows[4, 40] = 2.0
+    rows[4].view(torch.int16)[60_000] = -64                  # 0xFFC0: a negative quiet NaN
+    rows[5, 10], rows[5, 190_000] = float("inf"), float("nan")  # NaN above +inf
+    rows[6, 170_001] = 9.0                                   # only in the second round
+    rows[7, 100] = 3.0
+    rows[7, 180_000] = 3.0                                   # tie across rounds: first
+    got = greedy_argmax(rows.to(cuda_device)).cpu()
+    assert got.tolist() == [0, 3, 3, 8, 60_000, 190_000, 170_001, 100]
+    assert torch.equal(got, ref.greedy(rows))
+
+
+@pytest.mark.parametrize("vocab", [1, 5, 8, 13])
+def test_greedy_argmax_tiny_vocab(cuda_device, vocab):
+    g = torch.Generator().manual_seed(7 + vocab)
+    logits = _randn(4, vocab, gen=g)
+    logits[1, vocab - 1] = 30.0
+    buf = torch.zeros(4, 16, dtype=torch.bfloat16)  # row stride: a multiple of 8 elements
+    buf[:, :vocab] = logits
+    got = greedy_argmax(buf.to(cuda_device)[:, :vocab]).cpu()
+    assert torch.equal(got, ref.greedy(logits))
+    assert got[1].item() == vocab - 1
