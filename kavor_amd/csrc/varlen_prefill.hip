@@ -300,8 +300,9 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   const int ntiles_seq = (qlen + TOK - 1) / TOK;
-  // Grid-stride over query tiles (a sequence longer than the grid's max_seqlen_q is
-  // still covered); the last (longest) tiles go first.
+  // This unit's tile pairs jj, jj + J, jj + 2J, ... counted from the last tile (more
+  // than one only when max_seqlen_q understates the sequence); member 0 takes the later
+  // tile of each pair, member 1 the earlier one.
   for (int t = 2 * jj + member; t < ntiles_seq; t += 2 * J) {
     const int tile = ntiles_seq - 1 - t;
     const int q0 = tile * TOK;
