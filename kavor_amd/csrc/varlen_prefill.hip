@@ -244,8 +244,11 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   bool bad = false;
   if (PAGED && klen > p.max_blocks * p.block_size) bad = true;
 
-  // The first 64 block-table entries of the sequence, one per lane, read with readlane:
-  // a tile's block id then costs no memory round trip on the way to its K/V loads.
+  // Block-table entries 64 w .. 64 w + 63 of the sequence, one per lane, read with
+  // readlane: a tile's block id then costs no memory round trip on the way to its K/V
+  // loads.  Another window of 64 entries is loaded when the tiles move into it (once per
+  // 64 blocks, i.e. 16,384 keys at block size 256).
+  int bt_win = 0;
   int bt_lane = -1;
   if (PAGED && lane < p.max_blocks) bt_lane = p.block_tables[s * p.bt_stride + lane];
 
@@ -257,8 +260,12 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     bool blk_ok = true;
     if (PAGED) {
       const int lblk = kv0 / p.block_size;
-      int blk = lblk < 64 ? __builtin_amdgcn_readlane(bt_lane, lblk)
-                          : (lblk < p.max_blocks ? p.block_tables[s * p.bt_stride + lblk] : -1);
+      const int w = lblk >> 6;
+      if (w != bt_win) {  // uniform
+        bt_lane = 64 * w + lane < p.max_blocks ? p.block_tables[s * p.bt_stride + 64 * w + lane] : -1;
+        bt_win = w;
+      }
+      int blk = lblk < p.max_blocks ? __builtin_amdgcn_readlane(bt_lane, lblk & 63) : -1;
       if (blk < 0 || blk >= p.num_cache_blocks) {
         blk_ok = false;
         blk = 0;

@@ -198,12 +198,14 @@ def test_prefill_golden(cuda_device):
 
 
 def test_paged_table_longer_than_64_blocks(cuda_device):
-    """A context of more than 64 blocks: the first 64 block ids come from registers, the
-    rest from the table in memory (64-token pages, klen 4800 = 75 blocks)."""
-    qlens = [300, 40]
-    prefix = [4500, 4200]
+    """Contexts of more than 64 blocks: block ids come from a 64-entry window held in
+    registers, reloaded as the key tiles move into the next window (64-token pages: klen
+    4800 = 75 blocks, 9100 = 143 blocks = three windows), and back to the first window
+    for each query tile of the sequence."""
+    qlens = [300, 40, 200]
+    prefix = [4500, 4200, 8900]
     q, kc, vc, bt, cq, ck = _paged_case(250, qlens, prefix, 4, 2, 64)
-    assert bt.shape[1] >= 75
+    assert bt.shape[1] >= 143
     d = cuda_device
     out = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
     torch.cuda.synchronize()
