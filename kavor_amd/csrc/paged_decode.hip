@@ -404,37 +404,44 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 }
 
 // Combines the per-range partial states of sequences that span several ranges.
-// grid = (ceil(num_q_heads / 8), num_seqs), 1024 threads: 8 query heads x 128 dims,
-// one output element per thread (few, large workgroups: dispatch is the main cost).
+// grid = (ceil(num_q_heads / 4), num_seqs), 128 threads: 4 query heads x 32 threads,
+// 4 output elements (16-byte partial rows) per thread.  A quarter of the waves of one
+// thread per element: 175.0 -> 174.2 us per decode call on 256 sequences, and about
+// 1 us less for small batches.
 // The kernel is latency-bound: the first kSpecParts partial rows are loaded together
 // with the header words (their addresses do not depend on the part count), so the
 // common case costs one memory round trip; rows past the part count are ignored.
-constexpr int kMergeHeads = 8;
+constexpr int kMergeHeads = 4;
 constexpr int kSpecParts = 4;
-__global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_kernel(const DecodeParams p) {
+constexpr int kMergeThreads = kMergeHeads * kDecodeHeadDim / 4;  // 4 dims per thread
+__device__ __forceinline__ float4 fma4(float w, float4 o, float4 acc) {
+  return make_float4(acc.x + w * o.x, acc.y + w * o.y, acc.z + w * o.z, acc.w + w * o.w);
+}
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const DecodeParams p) {
   constexpr int D = kDecodeHeadDim;
-  const int h = blockIdx.x * kMergeHeads + static_cast<int>(threadIdx.x) / D;
+  const int h = blockIdx.x * kMergeHeads + static_cast<int>(threadIdx.x) / (D / 4);
   const int b = blockIdx.y;
-  const int d = threadIdx.x % D;
+  const int d = 4 * (threadIdx.x % (D / 4));
   if (h >= p.num_q_heads) return;
   const int64_t row0 = static_cast<int64_t>(b) * p.num_q_heads + h;
   const int64_t part_rows = static_cast<int64_t>(p.num_seqs) * p.num_q_heads;  // rows between parts
   const float* ml = p.part_ml + row0 * 2;
   const float* po = p.part_o + row0 * D + d;
   float2 st0[kSpecParts];
-  float ov0[kSpecParts];
+  float4 ov0[kSpecParts];
 #pragma unroll
   for (int k = 0; k < kSpecParts; ++k) {
     const int s = min(k, p.max_parts - 1);
     st0[k] = *reinterpret_cast<const float2*>(ml + 2 * s * part_rows);
-    ov0[k] = po[s * part_rows * D];
+    ov0[k] = *reinterpret_cast<const float4*>(po + s * part_rows * D);
   }
   const int cb = p.header[kHeaderInts + b], cb1 = p.header[kHeaderInts + b + 1];
   const int spr = p.header[0];
   // Consumes the rows here, before the branches below, so the compiler cannot sink their
   // loads under them: rows and header are then in flight together.
 #pragma unroll
-  for (int k = 0; k < kSpecParts; ++k) asm volatile("" ::"v"(st0[k].x), "v"(st0[k].y), "v"(ov0[k]));
+  for (int k = 0; k < kSpecParts; ++k)
+    asm volatile("" ::"v"(st0[k].x), "v"(st0[k].y), "v"(ov0[k].x), "v"(ov0[k].y), "v"(ov0[k].z), "v"(ov0[k].w));
   asm volatile("" ::"s"(spr));
   if (cb1 <= cb) return;  // no steps: written by the main kernel
   const int np = num_parts(cb, cb1, spr);
@@ -443,42 +450,44 @@ __global__ __launch_bounds__(kMergeHeads * kDecodeHeadDim) void decode_merge_ker
 #pragma unroll
   for (int k = 0; k < kSpecParts; ++k)
     if (k < np) mm = fmaxf(mm, st0[k].x);
-  float ll = 0.f, oo = 0.f;
+  float ll = 0.f;
+  float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int k = 0; k < kSpecParts; ++k) {
     if (k < np) {
       const float w = fast_exp2(st0[k].x - mm);
       ll += w * st0[k].y;
-      oo += w * ov0[k];
+      oo = fma4(w, ov0[k], oo);
     }
   }
   // Further parts (long sequences): batches of 8, all loads of a batch issued first.
   for (int s0 = kSpecParts; s0 < np; s0 += 8) {
     float2 st[8];
-    float ov[8];
+    float4 ov[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int s = min(s0 + k, np - 1);
       st[k] = *reinterpret_cast<const float2*>(ml + 2 * s * part_rows);
-      ov[k] = po[s * part_rows * D];
+      ov[k] = *reinterpret_cast<const float4*>(po + s * part_rows * D);
     }
     float bm = mm;
 #pragma unroll
     for (int k = 0; k < 8; ++k) bm = fmaxf(bm, st[k].x);
     const float alpha = fast_exp2(mm - bm);
     ll *= alpha;
-    oo *= alpha;
+    oo = make_float4(oo.x * alpha, oo.y * alpha, oo.z * alpha, oo.w * alpha);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (s0 + k < np) {
         const float w = fast_exp2(st[k].x - bm);
         ll += w * st[k].y;
-        oo += w * ov[k];
+        oo = fma4(w, ov[k], oo);
       }
     }
     mm = bm;
   }
-  p.out[b * p.o_seq_stride + h * p.o_head_stride + d] = f32_to_bf16(oo / ll);
+  uint16_t* o = p.out + b * p.o_seq_stride + h * p.o_head_stride + d;
+  *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(oo.x / ll, oo.y / ll), pack_bf16x2(oo.z / ll, oo.w / ll));
 }
 
 // Partial states per (sequence, query head): ranges hold at least kMinRangeTokens
@@ -525,7 +534,7 @@ static void launch_decode(DecodeParams p, int64_t max_tokens, hipStream_t s) {
   const int64_t grid = ranges * groups_per_range;
   hipLaunchKernelGGL((paged_decode_kernel<G, STEP>), dim3(static_cast<unsigned>(grid)), dim3(kDecodeThreads), 0, s, p);
   hipLaunchKernelGGL(decode_merge_kernel, dim3((p.num_q_heads + kMergeHeads - 1) / kMergeHeads, p.num_seqs),
-                     dim3(kMergeHeads * kDecodeHeadDim), 0, s, p);
+                     dim3(kMergeThreads), 0, s, p);
 }
 
 }  // namespace kvp
