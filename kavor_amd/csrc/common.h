@@ -28,14 +28,6 @@ inline bool mult8(int64_t stride) { return (stride & 7) == 0; }
 __device__ __forceinline__ float bf16_lo(u32 w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(u32 w) { return __uint_as_float(w & 0xffff0000u); }
 
-// fp32 -> bf16 with round-to-nearest-even; NaN stays NaN (quietened).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  u32 x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return static_cast<uint16_t>(x >> 16);
-}
-
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Two fp32 -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).

