@@ -87,6 +87,9 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 # ----------------------------------------------------------------------------- decode
 
 _workspaces: dict[int, torch.Tensor] = {}
+# Outgrown workspaces are kept, never freed: a graph captured before the growth still
+# launches the decode on the old buffer, and freed memory would be handed to new tensors.
+_retired_workspaces: list[torch.Tensor] = []
 
 
 def decode_workspace_bytes(max_num_seqs: int, num_q_heads: int, head_dim: int,
@@ -98,7 +101,9 @@ def decode_workspace_bytes(max_num_seqs: int, num_q_heads: int, head_dim: int,
 def reserve_decode_workspace(max_num_seqs: int, num_q_heads: int, head_dim: int,
                              max_blocks_per_seq: int, block_size: int,
                              device: torch.device | str | int) -> torch.Tensor:
-    """Allocates (or grows) the per-device decode workspace.  Call before graph capture."""
+    """Allocates (or grows) the per-device decode workspace.  Call before graph capture
+    with the largest batch a captured graph will use; an eager call that needs more grows
+    the workspace without freeing the one the graphs hold."""
     nbytes = decode_workspace_bytes(max_num_seqs, num_q_heads, head_dim, max_blocks_per_seq, block_size)
     dev = torch.device(device) if not isinstance(device, int) else torch.device("cuda", device)
     if dev.index is None:
@@ -109,6 +114,8 @@ def reserve_decode_workspace(max_num_seqs: int, num_q_heads: int, head_dim: int,
             raise RuntimeError(
                 "the paged-decode workspace must be reserved before graph capture "
                 f"({nbytes} bytes needed): call reserve_decode_workspace() first")
+        if ws is not None:
+            _retired_workspaces.append(ws)
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         _workspaces[dev.index] = ws
     return ws

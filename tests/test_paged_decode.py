@@ -164,6 +164,41 @@ def test_decode_graph_replay_matches_eager(cuda_device):
     torch.testing.assert_close(replay.cpu().float(), ref.paged_decode(q.cpu(), kc.cpu(), vc.cpu(), bt, ctx, SCALE), **TOL)
 
 
+
+def test_graph_keeps_its_workspace_when_an_eager_call_grows_it(cuda_device):
+    """A graph captured with the workspace reserved for its batch keeps launching on that
+    buffer after an eager call with a larger batch has grown the workspace.  The old
+    buffer must stay allocated: a tensor allocated after the growth (which the caching
+    allocator would place in a freed block of that size) is never written by a replay."""
+    from kavor_amd.layers import attention
+
+    d = cuda_device
+    B, hq, hkv, bs, width, nb = 8, 16, 8, 256, 16, 300
+    g = gen(23)
+    kc, vc = (t.to(d) for t in contiguous_caches(nb, bs, hkv, 128, g))
+    q = randn_bf16((B, hq, 128), g).to(d)
+    ctx = torch.randint(3000, 4096, (B,), generator=g, dtype=torch.int32)
+    bt = random_block_tables([int(c) for c in ctx], bs, nb, g, width=width)
+    ctx_d, bt_d = ctx.to(d), bt.to(d)
+    attention._workspaces.pop(d.index, None)  # start from a workspace sized for this batch
+    attention.reserve_decode_workspace(B, hq, 128, width, bs, d)
+    old_bytes = attention._workspaces[d.index].numel()
+    out = _decode(q, kc, vc, ctx_d, bt_d)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _decode(q, kc, vc, ctx_d, bt_d, out=out)
+    qb = randn_bf16((8 * B, hq, 128), g).to(d)
+    ctx_b = ctx.repeat(8).to(d)
+    bt_b = bt.repeat(8, 1).to(d)
+    _decode(qb, kc, vc, ctx_b, bt_b)  # grows the workspace
+    assert attention._workspaces[d.index].numel() > old_bytes
+    junk = torch.full((old_bytes,), 0x5A, dtype=torch.uint8, device=d)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    assert bool((junk == 0x5A).all())
+    assert bits_equal(out, _decode(q, kc, vc, ctx_d, bt_d))
+
 def _sampled_check(dev, q, kc, vc, bt, ctx, out, idx, bs):
     """Oracle check of a few sequences of a full-size run, gathering only their blocks."""
     ids, rows = [], []
