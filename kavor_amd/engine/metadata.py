@@ -24,6 +24,7 @@ writes as zeros, and block-table columns past a sequence's length are never read
 from __future__ import annotations
 
 from dataclasses import dataclass
+from itertools import chain
 
 import numpy as np
 import torch
@@ -135,26 +136,34 @@ class DecodeStaging:
     def fill(self, seqs: list[Sequence], block_size: int, bs: int) -> None:
         """Writes the host rows for `seqs`, pads rows len(seqs)..bs-1, and copies the
         buffer to the device (non-blocking, on the current stream).  The caller must
-        not refill before that copy has completed (the engine synchronises every step)."""
+        not refill before that copy has completed (the engine synchronises every step).
+
+        One pass over the sequences per field, then array operations: the ragged block
+        tables are scattered with one boolean-mask assignment (row i gets its table and
+        a -1 after it when it is narrower than the buffer; later columns keep stale
+        entries, which the kernels never read)."""
         n = len(seqs)
         if n > bs or bs > self.rows:
             raise ValueError(f"{n} sequences do not fit {bs} rows (staging has {self.rows})")
         ids, pos, slots, ctx = self._hf
-        tab = self._htab
-        for i, s in enumerate(seqs):
-            L = s.num_tokens
-            bt = s.block_table
-            nb = len(bt)
-            if nb * block_size < L or nb > self.width:
-                raise ValueError(f"sequence {s.seq_id}: {nb} blocks for {L} tokens "
-                                 f"(table width {self.width})")
-            ids[i] = s.last_token
-            pos[i] = L - 1
-            ctx[i] = L
-            slots[i] = bt[(L - 1) // block_size] * block_size + (L - 1) % block_size
-            tab[i, :nb] = bt
-            if nb < self.width:
-                tab[i, nb] = -1
+        L = np.fromiter((s.num_tokens for s in seqs), dtype=np.int64, count=n)
+        nbs = np.fromiter((len(s.block_table) for s in seqs), dtype=np.int64, count=n)
+        bad = (nbs * block_size < L) | (nbs > self.width)
+        if bad.any():
+            i = int(np.argmax(bad))
+            raise ValueError(f"sequence {seqs[i].seq_id}: {int(nbs[i])} blocks for {int(L[i])} tokens "
+                             f"(table width {self.width})")
+        flat = np.fromiter(chain.from_iterable(s.block_table for s in seqs), dtype=np.int32,
+                           count=int(nbs.sum()))
+        starts = np.cumsum(nbs) - nbs
+        self._htab[:n][np.arange(self.width)[None, :] < nbs[:, None]] = flat  # row-major = ragged order
+        short = nbs < self.width
+        self._htab[np.arange(n)[short], nbs[short]] = -1
+        last = L - 1
+        ids[:n] = np.fromiter((s.last_token for s in seqs), dtype=np.int64, count=n)
+        pos[:n] = last
+        ctx[:n] = L
+        slots[:n] = flat[starts + last // block_size].astype(np.int64) * block_size + last % block_size
         ids[n:bs] = 0
         pos[n:bs] = 0
         slots[n:bs] = -1
