@@ -548,10 +548,10 @@ def profile_run(dev, steps: int, warmup: int) -> int:
 
 PROFILE_CMDS = [
     "cd /tmp && export TMPDIR=/tmp",
-    "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/pmc_trace -o run -- python $R/bench.py --profile",
-    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_fetch -o run -- python $R/bench.py --profile",
-    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_write -o run -- python $R/bench.py --profile",
-    "python $R/bench.py --summarize $R/gpurun_out/pmc_trace $R/gpurun_out/pmc_fetch $R/gpurun_out/pmc_write",
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $OUT/pmc_trace -o run -- python $R/bench.py --profile",
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/pmc_fetch -o run -- python $R/bench.py --profile",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/pmc_write -o run -- python $R/bench.py --profile",
+    "python $R/bench.py --summarize $OUT/pmc_trace $OUT/pmc_fetch $OUT/pmc_write",
 ]
 
 PREFILL_PMC_PASSES = [
@@ -562,11 +562,11 @@ PREFILL_PMC_PASSES = [
 ]
 PREFILL_PMC_CMDS = [
     "cd /tmp && export TMPDIR=/tmp",
-    "rocprofv3 --pmc " + PREFILL_PMC_PASSES[0] + " --output-format csv -d $R/gpurun_out/ppmc_a -o run -- "
+    "rocprofv3 --pmc " + PREFILL_PMC_PASSES[0] + " --output-format csv -d $OUT/ppmc_a -o run -- "
     "python $R/bench.py --profile-prefill",
-    "rocprofv3 --pmc " + PREFILL_PMC_PASSES[1] + " --output-format csv -d $R/gpurun_out/ppmc_b -o run -- "
+    "rocprofv3 --pmc " + PREFILL_PMC_PASSES[1] + " --output-format csv -d $OUT/ppmc_b -o run -- "
     "python $R/bench.py --profile-prefill",
-    "python $R/bench.py --summarize-prefill-pmc $R/gpurun_out/ppmc_a $R/gpurun_out/ppmc_b",
+    "python $R/bench.py --summarize-prefill-pmc $OUT/ppmc_a $OUT/ppmc_b",
 ]
 
 
@@ -618,7 +618,7 @@ def summarize_prefill_pmc(dir_a: str, dir_b: str) -> int:
     lines = [
         f"# varlen_prefill_prefix_32seq counters: `{name}(kvp::PrefillParams)`",
         "",
-        "Commands (from the repository root on the GPU host, `R=$PWD`):",
+        "Commands (from the repository root on the GPU host, `R=$PWD`, `OUT` a directory for the raw results):",
         "",
         "```",
         *PREFILL_PMC_CMDS,
@@ -716,7 +716,7 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         avg_us = statistics.mean(d_us)
         traffic = (statistics.mean(fetch) if fetch else 0) + (statistics.mean(write) if write else 0)
         lines = [f"# {fname}: `{name}`", "",
-                 "Commands (from the repository root on the GPU host, `R=$PWD`):", "", "```"]
+                 "Commands (from the repository root on the GPU host, `R=$PWD`, `OUT` a directory for the raw results):", "", "```"]
         lines += PROFILE_CMDS + ["```", ""]
         med_us = statistics.median(d_us)
         lines += [f"- dispatches: {len(all_us)}; over the last {len(d_us)} (after the warm-up launches) "
@@ -750,8 +750,8 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
 
 E2E_PROFILE_CMDS = [
     "cd /tmp && export TMPDIR=/tmp",
-    "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/e2e_trace -o run -- python $R/bench.py --e2e-only",
-    "python $R/bench.py --summarize-e2e $R/gpurun_out/e2e_trace",
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $OUT/e2e_trace -o run -- python $R/bench.py --e2e-only",
+    "python $R/bench.py --summarize-e2e $OUT/e2e_trace",
 ]
 
 
@@ -777,7 +777,7 @@ def summarize_e2e(trace_dir: str) -> int:
         t, c = by.get(g, (0.0, 0))
         by[g] = (t + float(r["TotalDurationNs"]), c + int(r["Calls"]))
     lines = ["# e2e_qwen3_0.6b: GPU time of the end-to-end generation, by kernel", "",
-             "Commands (from the repository root on the GPU host, `R=$PWD`):", "", "```"]
+             "Commands (from the repository root on the GPU host, `R=$PWD`, `OUT` a directory for the raw results):", "", "```"]
     lines += E2E_PROFILE_CMDS + ["```", "",
                                  f"Total kernel time {total / 1e9:.3f} s (profiler overhead included; the "
                                  "untraced run's wall time is in bench.py's e2e_qwen3_0.6b field).", "",

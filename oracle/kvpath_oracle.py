@@ -1,7 +1,7 @@
 """CPU oracle of Kavor's paged KV-cache path.  TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import this
-module, and only as the checker (or the timed CPU baseline): the product path is
+module, and only to compute expected answers (or as the timed CPU baseline): the product path is
 kavor_amd/ over libkvpath.so and never calls into here.
 
 Each function restates the reference algorithm it names (paths are relative to the
