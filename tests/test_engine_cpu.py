@@ -101,6 +101,42 @@ def test_decode_staging_pads_rows(block_size):
         st.fill(seqs, block_size, 2)
 
 
+
+def test_decode_staging_refill_edges():
+    """Refilling the same staging buffer: each row gets its table and a -1 after it when
+    it is narrower than the buffer (columns past that keep stale entries, which the
+    kernels never read); a table as wide as the buffer gets no -1; rows past the batch
+    are padding; an empty batch pads every row; too few blocks or too many are refused."""
+    from kavor_amd.engine.metadata import DecodeStaging
+
+    bs = 64
+    seqs = [Sequence(list(range(n)), SamplingParams()) for n in (200, 70, 256)]
+    tables = [[5, 6, 7, 8], [9, 10], [11, 12, 13, 14]]
+    for s, t in zip(seqs, tables):
+        s.block_table = list(t)
+    st = DecodeStaging(rows=4, width=4, device="cpu", pin=False)
+    st.fill(seqs, bs, 4)
+    assert st._htab[:3].tolist() == [[5, 6, 7, 8], [9, 10, -1, 0], [11, 12, 13, 14]]
+    assert st.views(4).slot_mapping.tolist() == [8 * 64 + 7, 10 * 64 + 5, 14 * 64 + 63, -1]
+    # the same rows now hold shorter tables: stale columns past the -1 stay as they were
+    short = [Sequence(list(range(n)), SamplingParams()) for n in (3, 65)]
+    short[0].block_table, short[1].block_table = [1], [2, 3]
+    st.fill(short, bs, 3)
+    assert st._htab[:3].tolist() == [[1, -1, 7, 8], [2, 3, -1, 0], [11, 12, 13, 14]]
+    assert st.views(3).context_lens.tolist() == [3, 65, 0]
+    assert st.views(3).input_ids.tolist() == [2, 64, 0]
+    st.fill([], bs, 2)
+    assert st.views(2).slot_mapping.tolist() == [-1, -1]
+    assert st.views(2).context_lens.tolist() == [0, 0]
+    bad = Sequence(list(range(130)), SamplingParams())
+    bad.block_table = [1, 2]  # 2 pages of 64 hold 128 of 130 tokens
+    with pytest.raises(ValueError, match="2 blocks for 130 tokens"):
+        st.fill([bad], bs, 1)
+    wide = Sequence(list(range(10)), SamplingParams())
+    wide.block_table = [1, 2, 3, 4, 5]
+    with pytest.raises(ValueError, match="table width 4"):
+        st.fill([wide], bs, 1)
+
 def test_page_pool_views_match_layout():
     model = Qwen3ForCausalLM(TINY, "cpu")
     pool = CachePool(model, TINY.num_key_value_heads, TINY.head_dim, block_size=64)
