@@ -96,6 +96,35 @@ def test_preemption_recomputes(cuda_device):
         llm.exit()
 
 
+
+def test_batches_beyond_the_largest_graph(cuda_device, monkeypatch):
+    """With graphs captured only up to 4 sequences, a batch of 10 decodes eagerly and
+    grows the decode workspace past what the graphs were captured with; as sequences
+    finish the batch drops to 4 and below and the graphs replay on their own workspace.
+    Every token of both phases must match the reference."""
+    from kavor_amd.engine import model_runner
+    from kavor_amd.layers import attention
+
+    monkeypatch.setattr(model_runner, "MAX_GRAPH_BATCH", 4)
+    ws = attention._workspaces.pop(cuda_device.index, None)
+    if ws is not None:  # still used by graphs of other engines in this process
+        attention._retired_workspaces.append(ws)
+    llm = LLM(TINY, kvcache_block_size=64, max_model_len=1024, num_kvcache_blocks=128,
+              max_num_seqs=16, max_num_batched_tokens=2048, seed=0)
+    try:
+        assert max(llm.model_runner.graphs) == 4
+        captured = attention._workspaces[cuda_device.index].numel()
+        prompts = _prompts(6, [70, 5, 130, 64, 200, 33, 90, 1, 150, 260])
+        sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True)
+               for m in (6, 9, 12, 15, 18, 21, 24, 30, 36, 40)]
+        outs = llm.generate(prompts, sps)
+        decode_sizes = [s["seqs"] for s in llm.step_stats if not s["prefill"]]
+        assert max(decode_sizes) == 10 and min(decode_sizes) <= 4
+        assert attention._workspaces[cuda_device.index].numel() > captured  # grown by eager steps
+        _check(llm, prompts, outs)
+    finally:
+        llm.exit()
+
 def test_sampling_with_temperature_runs_and_eos_stops(graph_llm):
     prompts = _prompts(5, [40, 80])
     outs = graph_llm.generate(prompts, [SamplingParams(temperature=0.8, max_tokens=32),

@@ -180,7 +180,9 @@ def test_graph_keeps_its_workspace_when_an_eager_call_grows_it(cuda_device):
     ctx = torch.randint(3000, 4096, (B,), generator=g, dtype=torch.int32)
     bt = random_block_tables([int(c) for c in ctx], bs, nb, g, width=width)
     ctx_d, bt_d = ctx.to(d), bt.to(d)
-    attention._workspaces.pop(d.index, None)  # start from a workspace sized for this batch
+    ws = attention._workspaces.pop(d.index, None)  # start from a workspace sized for this batch
+    if ws is not None:  # graphs captured earlier in this process may still use it
+        attention._retired_workspaces.append(ws)
     attention.reserve_decode_workspace(B, hq, 128, width, bs, d)
     old_bytes = attention._workspaces[d.index].numel()
     out = _decode(q, kc, vc, ctx_d, bt_d)
