@@ -660,7 +660,7 @@ PROFILE_KERNELS = [
     ("paged_decode_qwen3_8b", "void kvp::paged_decode_kernel<4,", "decode_8b"),
     ("kv_append_4096tok", "void kvp::kv_append_kernel<128", "append"),
     ("varlen_prefill_prefix_32seq", "void kvp::varlen_prefill_kernel<2, true, true>", "prefill"),
-    ("qk_norm_rope_append_16384tok", "void kvp::(anonymous namespace)::qk_norm_rope_append_kernel<8>", "qk_norm_rope_append"),
+    ("qk_norm_rope_append_16384tok", "void kvp::(anonymous namespace)::qk_norm_rope_append_kernel<4>", "qk_norm_rope_append"),
     ("add_rmsnorm_16384x1024", "void kvp::(anonymous namespace)::rmsnorm_kernel<64, 2>", "add_rmsnorm"),
     ("silu_mul_16384x3072", "kvp::(anonymous namespace)::silu_mul_kernel", "silu_mul"),
     ("argmax_256x151936", "kvp::(anonymous namespace)::argmax_kernel", "argmax"),

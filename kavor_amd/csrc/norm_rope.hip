@@ -151,12 +151,13 @@ struct QkParams {
 // of its head, so its cos/sin values and norm weights are the same for every head: they
 // are loaded once per wave, and the wave issues the loads of its NB heads per row before
 // computing any of them.  The RoPE partner of element i (< 64) is i + 64, which lives in
-// lane j ^ 8 (DPP row_ror:8).  NB = 8 (one wave per token for Qwen3's 32 rows) suits
-// prefill-sized inputs; decode-sized ones take NB = 1 (8 waves per token), so that a
-// few tokens still spread over the GPU and each wave normalises one head per row instead
-// of eight in sequence (measured for one token: 6.3 us with NB = 8).
+// lane j ^ 8 (DPP row_ror:8).  NB = 4 (two waves per token for Qwen3's 32 rows) suits
+// prefill-sized inputs (16384 tokens: NB = 2, 4, 8 take 50, 46-47, 48 us); decode-sized
+// ones take NB = 1 (8 waves per token), so that a few tokens still spread over the GPU
+// and each wave normalises one head per row instead of several in sequence (measured for
+// one token: 6.3 us with NB = 8).
 
-constexpr int kQkWideTokens = 2048;  // token count from which NB = 8 is used
+constexpr int kQkWideTokens = 2048;  // token count from which NB = 4 is used
 
 __device__ __forceinline__ void norm_rope_head(float (&x)[8], const float (&w)[8], const float (&c)[8],
                                                const float (&sn)[8], bool first_half, bool pos_ok,
@@ -443,10 +444,10 @@ extern "C" int kvp_qk_norm_rope_append_bf16(
     return fail(KVP_EINVAL, "qkv row stride %lld is shorter than (hq + 2 hkv) * head_dim",
                 (long long)qkv_tok_stride);
   if (num_tokens == 0) return KVP_OK;
-  // Prefill-sized inputs: 8 head rows per 16-lane row (one wave per token for Qwen3);
+  // Prefill-sized inputs: 4 head rows per 16-lane row (two waves per token for Qwen3);
   // decode-sized ones: one head row per 16-lane row, several waves per token.
   const bool wide = num_tokens >= kQkWideTokens;
-  const int nb = wide ? 8 : 1;
+  const int nb = wide ? 4 : 1;
   const int64_t groups = (num_q_heads + 2 * num_kv_heads + 4 * nb - 1) / (4 * nb);
   const int64_t waves = static_cast<int64_t>(num_tokens) * groups;
   const int64_t grid = (waves + kThreads / 64 - 1) / (kThreads / 64);
@@ -458,7 +459,7 @@ extern "C" int kvp_qk_norm_rope_append_bf16(
              cache_block_stride, cache_slot_stride, cache_head_stride, num_cache_slots,
              slot_mapping, num_tokens, num_q_heads, num_kv_heads, block_size};
   if (wide)
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel<8>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
                        static_cast<hipStream_t>(stream), p);
   else
     hipLaunchKernelGGL(qk_norm_rope_append_kernel<1>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
