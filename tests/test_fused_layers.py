@@ -60,10 +60,15 @@ def _pool(num_blocks, bs, hkv, D, dev, gen):
 
 
 @pytest.mark.parametrize("T,hq,hkv", [(64, 32, 8), (300, 16, 8), (5, 16, 16), (1, 16, 8),
-                                      (2048, 16, 8), (2050, 32, 8)])
+                                      (3, 5, 1), (2048, 16, 8), (2050, 32, 8), (2050, 40, 8),
+                                      (2049, 5, 1)])
 def test_qk_norm_rope_append(cuda_device, T, hq, hkv):
-    """Below 2048 tokens each wave takes one head row per 16-lane row; from 2048 on, eight
-    (one wave per token for 32 rows; with 32 q + 8 + 8 rows, a second, half-empty group)."""
+    """A token's hq + 2*hkv head rows are cut into groups, one wave per group, each of the
+    wave's four 16-lane rows taking NB head rows: below 2048 tokens NB = 1 (groups of 4
+    rows), from 2048 on NB = 4 (groups of 16).  (3, 5, 1) has 7 rows, so its second
+    group of 4 has one idle row; (2050, 40, 8) has 56 rows, so the fourth group of 16 has
+    8 idle rows; (2049, 5, 1) fits in one group of 16 with 9 idle.  The idle rows load a
+    clamped head and store nothing."""
     D, bs, nb, max_pos = 128, 64, 40, 4096
     g = torch.Generator().manual_seed(2)
     qkv = _randn(T, (hq + 2 * hkv) * D, gen=g)
