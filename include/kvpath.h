@@ -78,7 +78,9 @@ int kvp_append_bf16(const void* key, int64_t key_tok_stride, int64_t key_head_st
  * blocks.  The caller allocates it once (before any graph capture), 256-byte aligned,
  * and passes it on every call; its contents need no initialisation.  It holds the
  * batch's step prefix sums and the fp32 partial states of sequences that the
- * work split divides.  Returns 0 for arguments the decode does not support.
+ * work split divides: at most (ranges + sequences) states per query head, with at most
+ * 1024 ranges per launch, whatever the context lengths (Qwen3-0.6B, 512 sequences:
+ * 12.8 MB).  Returns 0 for arguments the decode does not support.
  */
 size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q_heads, int32_t head_dim,
                                   int32_t max_blocks_per_seq, int32_t block_size);

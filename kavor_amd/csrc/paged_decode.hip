@@ -35,6 +35,11 @@
 //   and decode_merge_kernel combines them with the same online-softmax rule.  Partial
 //   traffic is about 2 states per group per sequence boundary: well under 1% of the KV
 //   bytes.
+//   Partial slots: the state that range r writes for sequence b goes to slot r + b.
+//   Sequence b's ranges are first_b .. last_b (first_b = cum_b / spr), and the next
+//   sequence with steps starts at a range >= last_b, so slots are unique, and one
+//   sequence's slots are consecutive.  A launch with R ranges over B sequences uses at
+//   most R + B slots of num_q_heads states each, whatever the context lengths.
 #include <math.h>
 
 #include <algorithm>
@@ -51,6 +56,9 @@ constexpr int kMinRangeTokens = 128;        // a range covers at least 128 token
 constexpr int kMinStepTokens = 16;           // smallest step (G = 8); G <= 4 steps 32 tokens
 constexpr int kMaxSeqsPerLaunch = 4096;      // size of the LDS prefix-sum table
 constexpr int kHeaderInts = 16;              // workspace header before the prefix table
+// Upper bound of the persistent grid.  Every variant holds 2 workgroups per CU on
+// MI355X (512 in all); the cap makes the workspace bound independent of the device.
+constexpr int kMaxDecodeGrid = 1024;
 
 struct DecodeParams {
   const uint16_t* q;
@@ -67,14 +75,13 @@ struct DecodeParams {
   int32_t num_kv_heads;
   int32_t block_size;
   int32_t max_blocks;
-  int32_t max_parts;  // partial states per (sequence, query head) the workspace holds
   int32_t step_tokens;  // tokens per step (the kernel's STEP)
   float scale_log2;   // softmax_scale * log2(e)
   uint16_t* out;
   int64_t o_seq_stride, o_head_stride;
   int32_t* header;  // [0] steps per range, [kHeaderInts ..] step prefix sums (B + 1)
-  float* part_o;    // [max_parts][num_seqs][num_q_heads][128]: part-major, so the parts in use
-  float* part_ml;   // [max_parts][num_seqs][num_q_heads][2] = (max, sum)   stay compact
+  float* part_o;    // [slot][num_q_heads][128], slot = range + sequence (ranges + B slots)
+  float* part_ml;   // [slot][num_q_heads][2] = (max, sum)
 };
 
 __device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
@@ -261,7 +268,7 @@ __device__ __forceinline__ void step_compute(const DecodeParams& p, const uint4 
 // Merges the 4 lane rows of the wave and writes the state of (b, kvh) for this range:
 // the bf16 output when one range covers the sequence, otherwise an fp32 partial.
 template <int G>
-__device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh, int part, bool single,
+__device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh, int slot, bool single,
                                            bool bad, int lane, float (&m)[G], float (&l)[G],
                                            float (&acc)[G][8]) {
   const int c = lane & 15;
@@ -292,7 +299,7 @@ __device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh
         o.w = pack_bf16x2(a[6] * inv, a[7] * inv);
         *reinterpret_cast<uint4*>(p.out + b * p.o_seq_stride + h * p.o_head_stride + 8 * c) = o;
       } else {
-        const int64_t row = (static_cast<int64_t>(part) * p.num_seqs + b) * p.num_q_heads + h;
+        const int64_t row = static_cast<int64_t>(slot) * p.num_q_heads + h;
         float4* dst = reinterpret_cast<float4*>(p.part_o + row * kDecodeHeadDim + 8 * c);
         dst[0] = make_float4(a[0], a[1], a[2], a[3]);
         dst[1] = make_float4(a[4], a[5], a[6], a[7]);
@@ -388,7 +395,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     if (seq_end || !more) {
       const int cb = s_cum[cur.b], cb1 = s_cum[cur.b + 1];
       const int np = num_parts(cb, cb1, spr);
-      emit_state<G>(p, cur.b, kvh, range - cb / spr, np == 1, cur.bad, lane, m, l, acc);
+      emit_state<G>(p, cur.b, kvh, range + cur.b, np == 1, cur.bad, lane, m, l, acc);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         m[g] = kMaxFloor;
@@ -416,9 +423,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 // 4 output elements (16-byte partial rows) per thread.  A quarter of the waves of one
 // thread per element: 175.0 -> 174.2 us per decode call on 256 sequences, and about
 // 1 us less for small batches.
-// The kernel is latency-bound: the first kSpecParts partial rows are loaded together
-// with the header words (their addresses do not depend on the part count), so the
-// common case costs one memory round trip; rows past the part count are ignored.
+// The kernel is latency-bound: it reads the sequence's step span and the steps per range
+// from the header (one round trip), then its first kSpecParts slots together (a second
+// one: the slots are consecutive and start at slot first_b + b); rows past the part count
+// are clamped onto the last part and ignored.
 constexpr int kMergeHeads = 4;
 constexpr int kSpecParts = 4;
 constexpr int kMergeThreads = kMergeHeads * kDecodeHeadDim / 4;  // 4 dims per thread
@@ -431,29 +439,23 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const Decod
   const int b = blockIdx.y;
   const int d = 4 * (threadIdx.x % (D / 4));
   if (h >= p.num_q_heads) return;
-  const int64_t row0 = static_cast<int64_t>(b) * p.num_q_heads + h;
-  const int64_t part_rows = static_cast<int64_t>(p.num_seqs) * p.num_q_heads;  // rows between parts
+  const int cb = load_uniform(p.header, kHeaderInts + b), cb1 = load_uniform(p.header, kHeaderInts + b + 1);
+  const int spr = load_uniform(p.header, 0);
+  if (cb1 <= cb) return;  // no steps: written by the main kernel
+  const int np = num_parts(cb, cb1, spr);
+  if (np <= 1) return;  // written by the main kernel
+  const int64_t row0 = static_cast<int64_t>(cb / spr + b) * p.num_q_heads + h;  // first slot's row
+  const int64_t hq = p.num_q_heads;  // rows between consecutive slots
   const float* ml = p.part_ml + row0 * 2;
   const float* po = p.part_o + row0 * D + d;
   float2 st0[kSpecParts];
   float4 ov0[kSpecParts];
 #pragma unroll
   for (int k = 0; k < kSpecParts; ++k) {
-    const int s = min(k, p.max_parts - 1);
-    st0[k] = *reinterpret_cast<const float2*>(ml + 2 * s * part_rows);
-    ov0[k] = *reinterpret_cast<const float4*>(po + s * part_rows * D);
+    const int s = min(k, np - 1);
+    st0[k] = *reinterpret_cast<const float2*>(ml + 2 * s * hq);
+    ov0[k] = *reinterpret_cast<const float4*>(po + s * hq * D);
   }
-  const int cb = p.header[kHeaderInts + b], cb1 = p.header[kHeaderInts + b + 1];
-  const int spr = p.header[0];
-  // Consumes the rows here, before the branches below, so the compiler cannot sink their
-  // loads under them: rows and header are then in flight together.
-#pragma unroll
-  for (int k = 0; k < kSpecParts; ++k)
-    asm volatile("" ::"v"(st0[k].x), "v"(st0[k].y), "v"(ov0[k].x), "v"(ov0[k].y), "v"(ov0[k].z), "v"(ov0[k].w));
-  asm volatile("" ::"s"(spr));
-  if (cb1 <= cb) return;  // no steps: written by the main kernel
-  const int np = num_parts(cb, cb1, spr);
-  if (np <= 1) return;  // written by the main kernel
   float mm = kMaxFloor;
 #pragma unroll
   for (int k = 0; k < kSpecParts; ++k)
@@ -475,8 +477,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const Decod
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int s = min(s0 + k, np - 1);
-      st[k] = *reinterpret_cast<const float2*>(ml + 2 * s * part_rows);
-      ov[k] = *reinterpret_cast<const float4*>(po + s * part_rows * D);
+      st[k] = *reinterpret_cast<const float2*>(ml + 2 * s * hq);
+      ov[k] = *reinterpret_cast<const float4*>(po + s * hq * D);
     }
     float bm = mm;
 #pragma unroll
@@ -498,21 +500,29 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const Decod
   *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(oo.x / ll, oo.y / ll), pack_bf16x2(oo.z / ll, oo.w / ll));
 }
 
-// Partial states per (sequence, query head): ranges hold at least kMinRangeTokens
-// tokens (whole steps of at least kMinStepTokens), so a sequence of up to max_tokens
-// tokens meets at most ceil(max_tokens / kMinRangeTokens) + 1 of them.
-static int64_t decode_max_parts(int64_t max_blocks, int64_t block_size) {
-  const int64_t tokens = max_blocks * block_size;
-  return (tokens + kMinRangeTokens - 1) / kMinRangeTokens + 1;
+constexpr int64_t kHeaderBytes = ((kHeaderInts + kMaxSeqsPerLaunch + 1) * 4 + 255) / 256 * 256;
+constexpr int64_t kStateBytes = (kDecodeHeadDim + 2) * 4;  // one (acc[128], max, sum) state
+
+// Ranges of one launch: the grid's groups, and no more than minimum-size ranges over the
+// largest possible work (max_tokens = sequences * table width * block_size).
+static int64_t range_cap(int64_t max_tokens) {
+  return std::max<int64_t>(1, (max_tokens + kMinRangeTokens - 1) / kMinRangeTokens);
 }
 
-static int64_t decode_workspace_need(int64_t seqs, int64_t q_heads, int64_t max_parts) {
-  const int64_t header = (kHeaderInts + kMaxSeqsPerLaunch + 1) * 4;
-  const int64_t header_padded = (header + 255) / 256 * 256;
-  return header_padded + seqs * q_heads * max_parts * (kDecodeHeadDim + 2) * 4;
+// Workspace bytes for a launch of `seqs` sequences over `ranges` ranges.
+static int64_t decode_workspace_need(int64_t seqs, int64_t q_heads, int64_t ranges) {
+  return kHeaderBytes + (ranges + seqs) * q_heads * kStateBytes;
 }
 
-// Workgroups of paged_decode_kernel<G> resident on the whole current device.
+// Workspace bytes that cover every launch of up to `seqs` sequences, on any device:
+// a launch has at most kMaxDecodeGrid ranges.
+static int64_t decode_workspace_bound(int64_t seqs, int64_t q_heads, int64_t max_blocks, int64_t block_size) {
+  const int64_t ranges = std::min<int64_t>(kMaxDecodeGrid, range_cap(seqs * max_blocks * block_size));
+  return decode_workspace_need(seqs, q_heads, ranges);
+}
+
+// Workgroups of paged_decode_kernel<G> resident on the whole current device (cached per
+// device once the queries succeed), capped at kMaxDecodeGrid.
 template <int G, int STEP>
 static int resident_workgroups() {
   static std::atomic<int> cached[16];
@@ -521,28 +531,145 @@ static int resident_workgroups() {
   int v = cached[dev].load(std::memory_order_relaxed);
   if (v > 0) return v;
   int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
+  bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
+  if (!ok) cus = 256;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<G, STEP>, kDecodeThreads, 0) !=
-          hipSuccess || per_cu <= 0)
+          hipSuccess || per_cu <= 0) {
     per_cu = 1;
-  v = cus * per_cu;
-  cached[dev].store(v, std::memory_order_relaxed);
+    ok = false;
+  }
+  v = std::min(cus * per_cu, kMaxDecodeGrid);
+  if (ok) cached[dev].store(v, std::memory_order_relaxed);
   return v;
 }
 
 template <int G, int STEP>
-static void launch_decode(DecodeParams p, int64_t max_tokens, hipStream_t s) {
+static int64_t decode_ranges(int num_kv_heads, int64_t max_tokens) {
+  const int64_t groups_per_range = (num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
+  return std::max<int64_t>(1, std::min<int64_t>(resident_workgroups<G, STEP>() / groups_per_range,
+                                                range_cap(max_tokens)));
+}
+
+static int64_t decode_ranges_for(int G, int num_kv_heads, int64_t max_tokens) {
+  switch (G) {
+    case 1: return decode_ranges<1, 32>(num_kv_heads, max_tokens);
+    case 2: return decode_ranges<2, 32>(num_kv_heads, max_tokens);
+    case 4: return decode_ranges<4, 32>(num_kv_heads, max_tokens);
+    default: return decode_ranges<8, kMinStepTokens>(num_kv_heads, max_tokens);
+  }
+}
+
+template <int G, int STEP>
+static void launch_decode(DecodeParams p, int64_t ranges, hipStream_t s) {
   const int64_t groups_per_range = (p.num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
-  const int64_t grid0 = resident_workgroups<G, STEP>();
-  // no more ranges than minimum-size ranges over the largest possible work
-  const int64_t max_ranges = std::max<int64_t>(1, (max_tokens + kMinRangeTokens - 1) / kMinRangeTokens);
   p.step_tokens = STEP;
-  const int64_t ranges = std::max<int64_t>(1, std::min<int64_t>(grid0 / groups_per_range, max_ranges));
-  const int64_t grid = ranges * groups_per_range;
-  hipLaunchKernelGGL((paged_decode_kernel<G, STEP>), dim3(static_cast<unsigned>(grid)), dim3(kDecodeThreads), 0, s, p);
+  hipLaunchKernelGGL((paged_decode_kernel<G, STEP>), dim3(static_cast<unsigned>(ranges * groups_per_range)),
+                     dim3(kDecodeThreads), 0, s, p);
   hipLaunchKernelGGL(decode_merge_kernel, dim3((p.num_q_heads + kMergeHeads - 1) / kMergeHeads, p.num_seqs),
                      dim3(kMergeThreads), 0, s, p);
+}
+
+struct DecodeArgs {
+  const void* q;
+  int64_t q_seq_stride, q_head_stride;
+  const void* k_cache;
+  const void* v_cache;
+  int64_t cache_block_stride, cache_slot_stride, cache_head_stride;
+  int32_t num_cache_blocks;
+  const int32_t* block_tables;
+  int64_t block_table_stride;
+  const int32_t* context_lens;
+  int32_t num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq;
+  float softmax_scale;
+  void* out;
+  int64_t out_seq_stride, out_head_stride;
+};
+
+// Host-side argument checks shared by both decode entry points (no HIP call).
+static int check_decode_args(const char* fn, const DecodeArgs& a) {
+  if (a.num_seqs < 0) return fail(KVP_EINVAL, "%s: num_seqs=%d < 0", fn, a.num_seqs);
+  if (a.head_dim != kDecodeHeadDim)
+    return fail(KVP_EUNSUPPORTED, "%s: head_dim=%d (supported: 128)", fn, a.head_dim);
+  if (a.num_kv_heads <= 0 || a.num_q_heads <= 0 || a.num_q_heads % a.num_kv_heads != 0)
+    return fail(KVP_EINVAL, "%s: num_q_heads=%d not a multiple of num_kv_heads=%d", fn, a.num_q_heads,
+                a.num_kv_heads);
+  const int G = a.num_q_heads / a.num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(KVP_EUNSUPPORTED, "%s: GQA ratio %d (supported: 1, 2, 4, 8)", fn, G);
+  if (a.block_size <= 0 || a.block_size % 64 != 0)
+    return fail(KVP_EINVAL, "%s: block_size=%d must be a positive multiple of 64", fn, a.block_size);
+  if (a.max_blocks_per_seq <= 0 || a.num_cache_blocks <= 0)
+    return fail(KVP_EINVAL, "%s: max_blocks_per_seq=%d num_cache_blocks=%d", fn, a.max_blocks_per_seq,
+                a.num_cache_blocks);
+  if (static_cast<int64_t>(a.max_blocks_per_seq) * a.block_size > (1ll << 30))
+    return fail(KVP_EINVAL, "%s: max_blocks_per_seq*block_size too large", fn);
+  if (a.block_table_stride < a.max_blocks_per_seq)
+    return fail(KVP_EINVAL, "%s: block_table_stride=%lld < max_blocks_per_seq=%d", fn,
+                static_cast<long long>(a.block_table_stride), a.max_blocks_per_seq);
+  if (!a.q || !a.k_cache || !a.v_cache || !a.block_tables || !a.context_lens || !a.out)
+    return fail(KVP_EINVAL, "%s: null pointer", fn);
+  if (!aligned16(a.q) || !aligned16(a.k_cache) || !aligned16(a.v_cache))
+    return fail(KVP_EINVAL, "%s: q and cache pointers must be 16-byte aligned", fn);
+  if (!aligned16(a.out) || (reinterpret_cast<uintptr_t>(a.block_tables) & 3u) ||
+      (reinterpret_cast<uintptr_t>(a.context_lens) & 3u))
+    return fail(KVP_EINVAL, "%s: misaligned out/block_tables/context_lens", fn);
+  if (!mult8(a.q_seq_stride) || !mult8(a.q_head_stride) || !mult8(a.cache_block_stride) ||
+      !mult8(a.cache_slot_stride) || !mult8(a.cache_head_stride) || !mult8(a.out_seq_stride) ||
+      !mult8(a.out_head_stride))
+    return fail(KVP_EINVAL, "%s: q, cache and out strides must be multiples of 8 elements", fn);
+  return KVP_OK;
+}
+
+// Enqueues the decode of a checked batch on `s` with `ws` as workspace (ws_bytes must
+// cover decode_workspace_need of every launch; checked by the callers).  Batches beyond
+// the LDS prefix table run as consecutive launches of up to 4096 sequences; they reuse
+// the workspace in stream order.
+static int enqueue_decode(const char* fn, const DecodeArgs& a, int64_t ranges, char* ws, hipStream_t s) {
+  const int G = a.num_q_heads / a.num_kv_heads;
+  for (int b0 = 0; b0 < a.num_seqs; b0 += kMaxSeqsPerLaunch) {
+    const int nb = std::min(kMaxSeqsPerLaunch, a.num_seqs - b0);
+    DecodeParams p;
+    p.q = static_cast<const uint16_t*>(a.q) + b0 * a.q_seq_stride;
+    p.q_seq_stride = a.q_seq_stride;
+    p.q_head_stride = a.q_head_stride;
+    p.k_cache = static_cast<const uint16_t*>(a.k_cache);
+    p.v_cache = static_cast<const uint16_t*>(a.v_cache);
+    p.blk_stride = a.cache_block_stride;
+    p.slot_stride = a.cache_slot_stride;
+    p.head_stride = a.cache_head_stride;
+    p.num_cache_blocks = a.num_cache_blocks;
+    p.block_tables = a.block_tables + b0 * a.block_table_stride;
+    p.bt_stride = a.block_table_stride;
+    p.context_lens = a.context_lens + b0;
+    p.num_seqs = nb;
+    p.num_q_heads = a.num_q_heads;
+    p.num_kv_heads = a.num_kv_heads;
+    p.block_size = a.block_size;
+    p.max_blocks = a.max_blocks_per_seq;
+    p.scale_log2 = a.softmax_scale * 1.4426950408889634f;
+    p.out = static_cast<uint16_t*>(a.out) + b0 * a.out_seq_stride;
+    p.o_seq_stride = a.out_seq_stride;
+    p.o_head_stride = a.out_head_stride;
+    p.header = reinterpret_cast<int32_t*>(ws);
+    p.part_o = reinterpret_cast<float*>(ws + kHeaderBytes);
+    p.part_ml = p.part_o + static_cast<size_t>(ranges + nb) * a.num_q_heads * kDecodeHeadDim;
+    switch (G) {
+      case 1: launch_decode<1, 32>(p, ranges, s); break;
+      case 2: launch_decode<2, 32>(p, ranges, s); break;
+      case 4: launch_decode<4, 32>(p, ranges, s); break;
+      default: launch_decode<8, kMinStepTokens>(p, ranges, s); break;
+    }
+    const int rc = launch_status(fn);
+    if (rc != KVP_OK) return rc;
+  }
+  return KVP_OK;
+}
+
+// Launch ranges for the batch's first (largest) launch.
+static int64_t batch_ranges(const DecodeArgs& a) {
+  const int nb = std::min(a.num_seqs, kMaxSeqsPerLaunch);
+  const int64_t max_tokens = static_cast<int64_t>(nb) * a.max_blocks_per_seq * a.block_size;
+  return decode_ranges_for(a.num_q_heads / a.num_kv_heads, a.num_kv_heads, max_tokens);
 }
 
 }  // namespace kvp
@@ -555,8 +682,7 @@ extern "C" size_t kvp_decode_workspace_bytes(int32_t max_num_seqs, int32_t num_q
       block_size <= 0)
     return 0;
   const int64_t seqs = std::min<int64_t>(max_num_seqs, kMaxSeqsPerLaunch);
-  return static_cast<size_t>(
-      decode_workspace_need(seqs, num_q_heads, decode_max_parts(max_blocks_per_seq, block_size)));
+  return static_cast<size_t>(decode_workspace_bound(seqs, num_q_heads, max_blocks_per_seq, block_size));
 }
 
 extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
@@ -570,92 +696,22 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
                                      float softmax_scale,
                                      void* out, int64_t out_seq_stride, int64_t out_head_stride,
                                      void* workspace, size_t workspace_bytes, void* stream) {
+  static const char fn[] = "kvp_paged_decode_bf16";
   clear_error();
-  if (num_seqs < 0) return fail(KVP_EINVAL, "kvp_paged_decode_bf16: num_seqs=%d < 0", num_seqs);
+  const DecodeArgs a = {q, q_seq_stride, q_head_stride, k_cache, v_cache, cache_block_stride,
+                        cache_slot_stride, cache_head_stride, num_cache_blocks, block_tables,
+                        block_table_stride, context_lens, num_seqs, num_q_heads, num_kv_heads,
+                        head_dim, block_size, max_blocks_per_seq, softmax_scale, out,
+                        out_seq_stride, out_head_stride};
+  int rc = check_decode_args(fn, a);
+  if (rc != KVP_OK) return rc;
   if (num_seqs == 0) return KVP_OK;
-  if (head_dim != kDecodeHeadDim)
-    return fail(KVP_EUNSUPPORTED, "kvp_paged_decode_bf16: head_dim=%d (supported: 128)", head_dim);
-  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: num_q_heads=%d not a multiple of num_kv_heads=%d",
-                num_q_heads, num_kv_heads);
-  const int G = num_q_heads / num_kv_heads;
-  if (G != 1 && G != 2 && G != 4 && G != 8)
-    return fail(KVP_EUNSUPPORTED, "kvp_paged_decode_bf16: GQA ratio %d (supported: 1, 2, 4, 8)", G);
-  if (block_size <= 0 || block_size % 64 != 0)
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: block_size=%d must be a positive multiple of 64",
-                block_size);
-  if (max_blocks_per_seq <= 0 || num_cache_blocks <= 0)
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: max_blocks_per_seq=%d num_cache_blocks=%d",
-                max_blocks_per_seq, num_cache_blocks);
-  if (static_cast<int64_t>(max_blocks_per_seq) * block_size > (1ll << 30))
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: max_blocks_per_seq*block_size too large");
-  if (block_table_stride < max_blocks_per_seq)
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: block_table_stride=%lld < max_blocks_per_seq=%d",
-                static_cast<long long>(block_table_stride), max_blocks_per_seq);
-  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: null pointer");
-  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: q and cache pointers must be 16-byte aligned");
-  if (!aligned16(out) || (reinterpret_cast<uintptr_t>(block_tables) & 3u) ||
-      (reinterpret_cast<uintptr_t>(context_lens) & 3u))
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: misaligned out/block_tables/context_lens");
-  if (!mult8(q_seq_stride) || !mult8(q_head_stride) || !mult8(cache_block_stride) ||
-      !mult8(cache_slot_stride) || !mult8(cache_head_stride) || !mult8(out_seq_stride) ||
-      !mult8(out_head_stride))
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: q, cache and out strides must be multiples of 8 elements");
-
   const int chunk_seqs = std::min(num_seqs, kMaxSeqsPerLaunch);
-  const int64_t max_parts = decode_max_parts(max_blocks_per_seq, block_size);
-  const size_t need = static_cast<size_t>(decode_workspace_need(chunk_seqs, num_q_heads, max_parts));
+  const size_t need =
+      static_cast<size_t>(decode_workspace_bound(chunk_seqs, num_q_heads, max_blocks_per_seq, block_size));
   if (!workspace || workspace_bytes < need)
-    return fail(KVP_EWORKSPACE, "kvp_paged_decode_bf16: workspace of %zu bytes, %zu needed",
-                workspace_bytes, need);
+    return fail(KVP_EWORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
-    return fail(KVP_EINVAL, "kvp_paged_decode_bf16: workspace must be 256-byte aligned");
-
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t header_bytes = (((kHeaderInts + kMaxSeqsPerLaunch + 1) * 4) + 255) / 256 * 256;
-  // Batches beyond the LDS prefix table run as consecutive launches of up to 4096
-  // sequences; they reuse the workspace in stream order.
-  for (int b0 = 0; b0 < num_seqs; b0 += kMaxSeqsPerLaunch) {
-    const int nb = std::min(kMaxSeqsPerLaunch, num_seqs - b0);
-    DecodeParams p;
-    p.q = static_cast<const uint16_t*>(q) + b0 * q_seq_stride;
-    p.q_seq_stride = q_seq_stride;
-    p.q_head_stride = q_head_stride;
-    p.k_cache = static_cast<const uint16_t*>(k_cache);
-    p.v_cache = static_cast<const uint16_t*>(v_cache);
-    p.blk_stride = cache_block_stride;
-    p.slot_stride = cache_slot_stride;
-    p.head_stride = cache_head_stride;
-    p.num_cache_blocks = num_cache_blocks;
-    p.block_tables = block_tables + b0 * block_table_stride;
-    p.bt_stride = block_table_stride;
-    p.context_lens = context_lens + b0;
-    p.num_seqs = nb;
-    p.num_q_heads = num_q_heads;
-    p.num_kv_heads = num_kv_heads;
-    p.block_size = block_size;
-    p.max_blocks = max_blocks_per_seq;
-    p.max_parts = static_cast<int32_t>(max_parts);
-    p.scale_log2 = softmax_scale * 1.4426950408889634f;
-    p.out = static_cast<uint16_t*>(out) + b0 * out_seq_stride;
-    p.o_seq_stride = out_seq_stride;
-    p.o_head_stride = out_head_stride;
-    char* ws = static_cast<char*>(workspace);
-    p.header = reinterpret_cast<int32_t*>(ws);
-    p.part_o = reinterpret_cast<float*>(ws + header_bytes);
-    p.part_ml = p.part_o + static_cast<size_t>(nb) * num_q_heads * max_parts * kDecodeHeadDim;
-
-    const int64_t max_tokens = static_cast<int64_t>(nb) * max_blocks_per_seq * block_size;
-    switch (G) {
-      case 1: launch_decode<1, 32>(p, max_tokens, s); break;
-      case 2: launch_decode<2, 32>(p, max_tokens, s); break;
-      case 4: launch_decode<4, 32>(p, max_tokens, s); break;
-      default: launch_decode<8, kMinStepTokens>(p, max_tokens, s); break;
-    }
-    const int rc = launch_status("kvp_paged_decode_bf16");
-    if (rc != KVP_OK) return rc;
-  }
-  return KVP_OK;
+    return fail(KVP_EINVAL, "%s: workspace must be 256-byte aligned", fn);
+  return enqueue_decode(fn, a, batch_ranges(a), static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
 }

@@ -77,14 +77,18 @@ def test_decode_rejects_bad_arguments_on_host():
 
 
 def test_decode_workspace_size_formula():
-    # 256-byte-aligned header (16 ints + a 4097-entry prefix table), then per (sequence,
-    # query head) up to ceil(max_tokens / 128) + 1 partial states of 130 floats
+    # 256-byte-aligned header (16 ints + a 4097-entry prefix table), then one state of 130
+    # floats per query head for each of (ranges + sequences) slots; a launch has at most
+    # min(1024, ceil(sequences * width * block_size / 128)) ranges
     header = ((16 + 4097) * 4 + 255) // 256 * 256
-    parts = -(-(16 * 256) // 128) + 1
-    assert _lib.lib().kvp_decode_workspace_bytes(512, 16, 128, 16, 256) == header + 512 * 16 * parts * 130 * 4
-    assert _lib.lib().kvp_decode_workspace_bytes(9000, 16, 128, 16, 256) == header + 4096 * 16 * parts * 130 * 4
-    assert _lib.lib().kvp_decode_workspace_bytes(0, 16, 128, 16, 256) == 0
-    assert _lib.lib().kvp_decode_workspace_bytes(8, 16, 64, 16, 256) == 0
+    state = 130 * 4
+    size = _lib.lib().kvp_decode_workspace_bytes
+    assert size(512, 16, 128, 16, 256) == header + (1024 + 512) * 16 * state
+    assert size(9000, 16, 128, 16, 256) == header + (1024 + 4096) * 16 * state
+    assert size(2, 16, 128, 1, 64) == header + (1 + 2) * 16 * state
+    assert size(6, 32, 128, 2, 256) == header + (24 + 6) * 32 * state
+    assert size(0, 16, 128, 16, 256) == 0
+    assert size(8, 16, 64, 16, 256) == 0
 
 
 def _prefill(**over):
