@@ -115,6 +115,31 @@ int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_t q_head_st
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * kvp_paged_decode_bf16 without a workspace argument: the decode's partial states live
+ * in a static 32 MiB device array of the library (one per GPU, held until the process
+ * ends), so the call allocates nothing and needs no caller buffer.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, semantics and results as kvp_paged_decode_bf16 (bit for bit).  A batch
+ * whose partial states do not fit (about (512 + num_seqs) * num_q_heads * 520 bytes on
+ * MI355X; Qwen3-0.6B at 512 sequences takes 8.5 MB) returns KVP_EWORKSPACE before any
+ * launch.  Every call on one GPU shares that GPU's array, so calls that overlap on one
+ * GPU (different streams or threads without ordering) race; calls ordered on one
+ * stream do not.  The array needs no clearing between calls.
+ */
+int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                                  const void* k_cache, const void* v_cache,
+                                  int64_t cache_block_stride, int64_t cache_slot_stride,
+                                  int64_t cache_head_stride, int32_t num_cache_blocks,
+                                  const int32_t* block_tables, int64_t block_table_stride,
+                                  const int32_t* context_lens, int32_t num_seqs,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t block_size, int32_t max_blocks_per_seq,
+                                  float softmax_scale,
+                                  void* out, int64_t out_seq_stride, int64_t out_head_stride,
+                                  void* stream);
+
+/*
  * Variable-length prefill attention over packed sequences (bf16 MFMA).
  * Sequence s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1]) of q and keys
  * 0 .. klen_s-1 with klen_s = cu_seqlens_k[s+1] - cu_seqlens_k[s].  With causal != 0

@@ -672,6 +672,35 @@ static int64_t batch_ranges(const DecodeArgs& a) {
   return decode_ranges_for(a.num_q_heads / a.num_kv_heads, a.num_kv_heads, max_tokens);
 }
 
+// ---------------------------------------------------------------- no-allocation variant
+
+// Workspace of kvp_paged_decode_bf16_noalloc: one per device, held until the process ends.
+constexpr size_t kScratchBytes = 32u << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+// Device address of this device's `scratch`, looked up once per device with that device
+// current.  The host-side symbol is not a device address and is never passed to a kernel.
+static int scratch_address(const char* fn, char** out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<char*> addr[kMaxDevices];
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(static_cast<int>(err), "%s: hipGetDevice: %s", fn, hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices) return fail(KVP_EINVAL, "%s: device %d beyond %d", fn, dev, kMaxDevices);
+  char* ptr = addr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    void* sym = nullptr;
+    err = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !sym)
+      return fail(err != hipSuccess ? static_cast<int>(err) : KVP_EINVAL, "%s: hipGetSymbolAddress(scratch): %s",
+                  fn, hipGetErrorString(err));
+    ptr = static_cast<char*>(sym);
+    addr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return KVP_OK;
+}
+
 }  // namespace kvp
 
 using namespace kvp;
@@ -714,4 +743,38 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
     return fail(KVP_EINVAL, "%s: workspace must be 256-byte aligned", fn);
   return enqueue_decode(fn, a, batch_ranges(a), static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                                             const void* k_cache, const void* v_cache,
+                                             int64_t cache_block_stride, int64_t cache_slot_stride,
+                                             int64_t cache_head_stride, int32_t num_cache_blocks,
+                                             const int32_t* block_tables, int64_t block_table_stride,
+                                             const int32_t* context_lens, int32_t num_seqs,
+                                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                             int32_t block_size, int32_t max_blocks_per_seq,
+                                             float softmax_scale,
+                                             void* out, int64_t out_seq_stride, int64_t out_head_stride,
+                                             void* stream) {
+  static const char fn[] = "kvp_paged_decode_bf16_noalloc";
+  clear_error();
+  const DecodeArgs a = {q, q_seq_stride, q_head_stride, k_cache, v_cache, cache_block_stride,
+                        cache_slot_stride, cache_head_stride, num_cache_blocks, block_tables,
+                        block_table_stride, context_lens, num_seqs, num_q_heads, num_kv_heads,
+                        head_dim, block_size, max_blocks_per_seq, softmax_scale, out,
+                        out_seq_stride, out_head_stride};
+  int rc = check_decode_args(fn, a);
+  if (rc != KVP_OK) return rc;
+  if (num_seqs == 0) return KVP_OK;
+  const int64_t ranges = batch_ranges(a);
+  const int64_t need = decode_workspace_need(std::min(num_seqs, kMaxSeqsPerLaunch), num_q_heads, ranges);
+  if (need > static_cast<int64_t>(kScratchBytes))
+    return fail(KVP_EWORKSPACE,
+                "%s: %d sequences x %d query heads need %lld bytes of decode scratch; the static scratch "
+                "holds %zu (use kvp_paged_decode_bf16 with a caller workspace)",
+                fn, std::min(num_seqs, kMaxSeqsPerLaunch), num_q_heads, static_cast<long long>(need), kScratchBytes);
+  char* ws = nullptr;
+  rc = scratch_address(fn, &ws);
+  if (rc != KVP_OK) return rc;
+  return enqueue_decode(fn, a, ranges, ws, static_cast<hipStream_t>(stream));
 }

@@ -76,6 +76,23 @@ def test_decode_rejects_bad_arguments_on_host():
     assert b"workspace" in _lib.lib().kvp_last_error()
 
 
+def test_noalloc_decode_rejects_bad_arguments_on_host():
+    lib = _lib.lib()
+    args = dict(q=16, qs=2048, qh=128, kc=16, vc=16, bstr=524288, sstr=1024, hstr=128, nblk=64,
+                bt=16, bts=16, ctx=16, b=4, hq=16, hkv=8, d=128, bs=256, maxb=16, scale=0.088,
+                out=16, os=2048, oh=128, stream=None)
+
+    def call(**over):
+        return lib.kvp_paged_decode_bf16_noalloc(*dict(args, **over).values())
+
+    assert call(b=0) == _lib.KVP_OK
+    assert call(d=64) == _lib.KVP_EUNSUPPORTED
+    assert call(hq=24) == _lib.KVP_EUNSUPPORTED
+    assert call(bs=100) == _lib.KVP_EINVAL
+    assert call(out=None) == _lib.KVP_EINVAL
+    assert b"kvp_paged_decode_bf16_noalloc" in lib.kvp_last_error()
+
+
 def test_decode_workspace_size_formula():
     # 256-byte-aligned header (16 ints + a 4097-entry prefix table), then one state of 130
     # floats per query head for each of (ranges + sequences) slots; a launch has at most
