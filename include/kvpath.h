@@ -243,9 +243,15 @@ int kvp_silu_mul_bf16(const void* gate_up, int64_t gate_up_tok_stride, void* out
  * Greedy sampling: out[r] = index of the largest of logits[r, 0:vocab] (int64), the first
  * one on ties, NaN counting as largest (torch.argmax semantics).  Replaces the
  * temperature-0 branch of _sample_kernel (kavor/layers/sampler.py:7-45).
+ * The workspace is optional (NULL allowed): with at least
+ * kvp_argmax_workspace_bytes(num_rows) bytes (8-byte aligned, no initialisation needed),
+ * batches of fewer than 192 rows split each row over several workgroups, which fills
+ * the GPU (e.g. 9.6 -> 5.3 us for one 151936-wide row); without it every row is scanned
+ * by one workgroup.  The result is the same either way.
  */
+size_t kvp_argmax_workspace_bytes(int32_t num_rows);
 int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t num_rows, int32_t vocab,
-                    int64_t* out, void* stream);
+                    int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

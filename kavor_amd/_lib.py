@@ -97,9 +97,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_void_p, _i64, _c_void_p, _i64,  # gate_up, gate_up_tok_stride, out, out_tok_stride
         _i32, _i32, _c_void_p,            # num_tokens, intermediate, stream
     ]),
+    "kvp_argmax_workspace_bytes": (_size_t, [_i32]),
     "kvp_argmax_bf16": (ctypes.c_int, [
         _c_void_p, _i64, _i32, _i32,      # logits, row_stride, num_rows, vocab
-        _c_void_p, _c_void_p,             # out (int64), stream
+        _c_void_p,                        # out (int64)
+        _c_void_p, _size_t, _c_void_p,    # workspace, workspace_bytes, stream
     ]),
 }
 

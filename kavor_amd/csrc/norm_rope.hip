@@ -278,17 +278,32 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(SiluParams p) {
 
 // ------------------------------------------------------------------ argmax
 
+// Whole rows: one 1024-thread workgroup per row.  16-byte loads per thread per round:
+// over 256 rows of 151936 (six rotating inputs, so HBM-resident) 3 per round 15.5 us,
+// 4 15.9 us, 8 16.9 us; deeper rounds leave more of the last round's loads clamped onto
+// the row's final chunk.  A plain streaming read of the same 78 MB (same grid shapes)
+// takes 12.4 us: keeping the winning chunk's bits costs about 1 us and the reduction
+// epilogue with the end-of-kernel write-back about 1.8 us.
 constexpr int kArgmaxThreads = 1024;
-// 16-byte loads per thread per round.  Over 256 rows of 151936 (six rotating inputs, so
-// HBM-resident): 3 per round 15.5 us, 4 15.9 us, 8 16.9 us; deeper rounds leave more of
-// the last round's loads clamped onto the row's final chunk.
 constexpr int kArgmaxBatch = 3;
+// Split rows: below kArgmaxSplitRows rows, each row is cut into S segments of one
+// 256-thread workgroup each (S up to 16, so that rows * S reaches about 1024 workgroups);
+// for a 151936-wide row at 8 or more segments every thread loads all of its chunks in
+// one round.  Each workgroup writes its best as an ordered 64-bit key and
+// argmax_merge_kernel takes the largest key of each row.  Measured over rotating inputs of width 151936: 1 row 9.6 -> 5.3 us,
+// 16 rows 10.5 -> 6.1 us, 64 rows 11.6 -> 8.3 us, 128 rows 12.2 -> 10.9 us; at 256 rows
+// the split (2 segments) is 2% slower than whole rows.
+constexpr int kArgmaxSplitThreads = 256;
+constexpr int kArgmaxSplitRows = 192;
+constexpr int kArgmaxMaxSegments = 16;
 
 struct ArgmaxParams {
   const uint16_t* logits;
   int64_t row_stride;
   int vocab;
-  int64_t* out;
+  int segments;                 // workgroups per row (1: whole rows)
+  int64_t* out;                 // whole rows: the index
+  unsigned long long* keys;     // split rows: [row][segment] keys
 };
 
 // (v, i) beats (b, j): NaN above every number (as torch.argmax), then larger value, then
@@ -303,32 +318,52 @@ __device__ __forceinline__ float max_nan(float a, float b) {
   return __builtin_elementwise_maximum(a, b);  // NaN-propagating (v_maximum3_f32)
 }
 
-// One workgroup per row.  Per chunk of 8 values a lane keeps, without branches, the
-// NaN-propagating maximum over its chunks, the chunk that first reached it and that
-// chunk's raw bits; the index inside the kept chunk is found once at the end.  A lane's
-// chunks come in increasing index order and only a strictly greater maximum (or a first
-// NaN) replaces the kept chunk, so ties keep the first occurrence.
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(ArgmaxParams p) {
-  const uint16_t* row = p.logits + blockIdx.x * p.row_stride;
+// Orders (v, i) as `beats` does, as one unsigned 64-bit integer: the value's bits made
+// monotonic (NaN on top, -0 folded onto +0) above the complemented index.  0 is below
+// every real key and marks an empty segment.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+  u32 ord;
+  if (v != v) {
+    ord = 0xffffffffu;
+  } else {
+    u32 b = __float_as_uint(v);
+    if (b == 0x80000000u) b = 0;
+    ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return (static_cast<unsigned long long>(ord) << 32) | (0xffffffffu - static_cast<u32>(i));
+}
+
+// Per chunk of 8 values a lane keeps, without branches, the NaN-propagating maximum over
+// its chunks, the chunk that first reached it and that chunk's raw bits; the index inside
+// the kept chunk is found once at the end.  A lane's chunks come in increasing index
+// order and only a strictly greater maximum (or a first NaN) replaces the kept chunk, so
+// ties keep the first occurrence.  The row segment is chunks [cbeg, cend); the
+// (vocab % 8)-value tail goes to the last segment.
+template <int THREADS, int BATCH, bool SPLIT>
+__global__ __launch_bounds__(THREADS) void argmax_kernel(ArgmaxParams p) {
+  const int r = SPLIT ? static_cast<int>(blockIdx.x) / p.segments : static_cast<int>(blockIdx.x);
+  const int seg = SPLIT ? static_cast<int>(blockIdx.x) - r * p.segments : 0;
+  const uint16_t* row = p.logits + r * p.row_stride;
   const int nvec = p.vocab >> 3;
+  const int per = SPLIT ? (nvec + p.segments - 1) / p.segments : nvec;
+  const int cbeg = seg * per, cend = min(nvec, cbeg + per);
   float cmax = -__builtin_inff();
   int bc = -1;
   uint4 bw = make_uint4(0, 0, 0, 0);
-  // kArgmaxBatch 16-byte loads per thread in flight before any is scanned; indices past
-  // the row are clamped onto its last chunk and skipped.
-  for (int c0 = threadIdx.x; c0 < nvec; c0 += kArgmaxThreads * kArgmaxBatch) {
-    uint4 w[kArgmaxBatch];
+  // BATCH 16-byte loads per thread in flight before any is scanned; indices past the
+  // segment are clamped onto its last chunk and skipped.
+  for (int c0 = cbeg + threadIdx.x; c0 < cend; c0 += THREADS * BATCH) {
+    uint4 w[BATCH];
 #pragma unroll
-    for (int u = 0; u < kArgmaxBatch; ++u)
-      w[u] = load16_nt(row + 8 * min(c0 + u * kArgmaxThreads, nvec - 1));
+    for (int u = 0; u < BATCH; ++u) w[u] = load16_nt(row + 8 * min(c0 + u * THREADS, cend - 1));
 #pragma unroll
-    for (int u = 0; u < kArgmaxBatch; ++u) {
-      const int c = c0 + u * kArgmaxThreads;
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = c0 + u * THREADS;
       float f[8];
       unpack8(w[u], f);
       const float m = max_nan(max_nan(max_nan(f[0], f[1]), max_nan(f[2], f[3])),
                               max_nan(max_nan(f[4], f[5]), max_nan(f[6], f[7])));
-      const bool up = c < nvec && (bc < 0 || (m != m ? cmax == cmax : m > cmax));
+      const bool up = c < cend && (bc < 0 || (m != m ? cmax == cmax : m > cmax));
       cmax = up ? m : cmax;
       bc = up ? c : bc;
       bw.x = up ? w[u].x : bw.x;
@@ -352,7 +387,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(ArgmaxParams p) 
     bi = 8 * bc + e0;
   }
   const int tail = p.vocab - 8 * nvec;
-  if (static_cast<int>(threadIdx.x) < tail) {
+  if ((!SPLIT || seg == p.segments - 1) && static_cast<int>(threadIdx.x) < tail) {
     const int i = 8 * nvec + threadIdx.x;
     const float f = __uint_as_float(static_cast<u32>(row[i]) << 16);
     if (beats(f, i, best, bi)) { best = f; bi = i; }
@@ -363,16 +398,27 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(ArgmaxParams p) 
     const int oi = __shfl_xor(bi, off);
     if (beats(ob, oi, best, bi)) { best = ob; bi = oi; }
   }
-  __shared__ float s_best[kArgmaxThreads / 64];
-  __shared__ int s_idx[kArgmaxThreads / 64];
+  __shared__ float s_best[THREADS / 64];
+  __shared__ int s_idx[THREADS / 64];
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { s_best[wave] = best; s_idx[wave] = bi; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kArgmaxThreads / 64; ++w)
+    for (int w = 1; w < THREADS / 64; ++w)
       if (beats(s_best[w], s_idx[w], best, bi)) { best = s_best[w]; bi = s_idx[w]; }
-    p.out[blockIdx.x] = bi;
+    if (SPLIT) p.keys[blockIdx.x] = bi == 0x7fffffff ? 0ull : argmax_key(best, bi);
+    else p.out[blockIdx.x] = bi;
   }
+}
+
+// One thread per row: the largest of the row's segment keys, back to its index.
+__global__ __launch_bounds__(256) void argmax_merge_kernel(ArgmaxParams p, int rows) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const unsigned long long* k = p.keys + static_cast<int64_t>(r) * p.segments;
+  unsigned long long m = 0;
+  for (int s = 0; s < p.segments; ++s) m = k[s] > m ? k[s] : m;
+  p.out[r] = 0xffffffffu - static_cast<u32>(m & 0xffffffffu);
 }
 
 }  // namespace
@@ -489,8 +535,21 @@ extern "C" int kvp_silu_mul_bf16(const void* gate_up, int64_t gate_up_tok_stride
   return launch_status("silu_mul_kernel");
 }
 
+// Segments per row for split rows (1: whole rows).
+static int argmax_segments(int32_t num_rows) {
+  if (num_rows >= kArgmaxSplitRows) return 1;
+  return std::min(kArgmaxMaxSegments, std::max(2, 1024 / std::max(num_rows, 1)));
+}
+
+extern "C" size_t kvp_argmax_workspace_bytes(int32_t num_rows) {
+  if (num_rows <= 0) return 0;
+  const int s = argmax_segments(num_rows);
+  return s == 1 ? 0 : static_cast<size_t>(num_rows) * s * sizeof(unsigned long long);
+}
+
 extern "C" int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t num_rows,
-                               int32_t vocab, int64_t* out, void* stream) {
+                               int32_t vocab, int64_t* out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
   clear_error();
   if (!logits || !out) return fail(KVP_EINVAL, "null pointer");
   if (num_rows < 0 || vocab < 1) return fail(KVP_EINVAL, "bad shape");
@@ -498,8 +557,25 @@ extern "C" int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t n
     return fail(KVP_EINVAL, "logits must be 16-byte aligned with a row stride >= vocab that is a "
                 "multiple of 8 elements");
   if (num_rows == 0) return KVP_OK;
-  ArgmaxParams p{static_cast<const uint16_t*>(logits), row_stride, vocab, out};
-  hipLaunchKernelGGL(argmax_kernel, dim3(num_rows), dim3(kArgmaxThreads), 0,
-                     static_cast<hipStream_t>(stream), p);
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 7u))
+    return fail(KVP_EINVAL, "workspace must be 8-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  ArgmaxParams p{static_cast<const uint16_t*>(logits), row_stride, vocab, argmax_segments(num_rows), out,
+                 static_cast<unsigned long long*>(workspace)};
+  // Split rows need the caller's workspace; without one (or too small) rows stay whole.
+  if (p.segments > 1 && workspace && workspace_bytes >= kvp_argmax_workspace_bytes(num_rows)) {
+    const int per = (vocab / 8 + p.segments - 1) / p.segments;  // chunks per segment
+    if (per > 5 * kArgmaxSplitThreads)
+      hipLaunchKernelGGL((argmax_kernel<kArgmaxSplitThreads, 10, true>), dim3(num_rows * p.segments),
+                         dim3(kArgmaxSplitThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((argmax_kernel<kArgmaxSplitThreads, 5, true>), dim3(num_rows * p.segments),
+                         dim3(kArgmaxSplitThreads), 0, s, p);
+    hipLaunchKernelGGL(argmax_merge_kernel, dim3((num_rows + 255) / 256), dim3(256), 0, s, p, num_rows);
+    return launch_status("argmax_kernel (split rows)");
+  }
+  p.segments = 1;
+  hipLaunchKernelGGL((argmax_kernel<kArgmaxThreads, kArgmaxBatch, false>), dim3(num_rows), dim3(kArgmaxThreads), 0,
+                     s, p);
   return launch_status("argmax_kernel");
 }

@@ -11,15 +11,18 @@ the shared-memory control plane of :85-106 has nothing to do):
   sequence on its own consecutive blocks) and decode (all slots 0, context length 1);
 - capture_cudagraph (:264-327): one hipGraph per batch size in
   [1, 2, 4, 8] + range(16, max_bs + 1, 16) (+ max_bs), sharing one memory pool,
-  captured with all-zero metadata and including the LM head; the paged-decode
-  workspace is reserved before capture;
+  captured with all-zero metadata; as at tensor_parallel_size 1 there (:280-310), the
+  LM head and the greedy sampler are inside the graph, which leaves the tokens in a
+  persistent sampled_tokens buffer; the paged-decode workspace is reserved before
+  capture;
 - run / run_model (:213-262): prefill runs eagerly, decode replays the smallest graph
   that holds the batch, padding rows carry slot -1 and context length 0.
 
 Per-step metadata travels in one host-to-device copy (kavor_amd.engine.metadata); the
 prefill always carries block tables because the model appends k / v before attention
-and attention reads the pages.  Sampling runs after the graph: greedy batches take one
-argmax pass over the logits.
+and attention reads the pages.  An all-greedy decode batch reads its tokens from the
+graph's sampled_tokens; a batch with a temperature above 0 samples from the graph's
+logits after the replay (the reference's graph samples every temperature inside).
 """
 
 from __future__ import annotations
@@ -37,6 +40,7 @@ from kavor_amd.engine.qwen3 import Qwen3ForCausalLM, load_checkpoint_tensors
 from kavor_amd.engine.sampler import Sampler
 from kavor_amd.engine.sequence import Sequence
 from kavor_amd.layers.attention import reserve_decode_workspace
+from kavor_amd.layers.fused import argmax_workspace, greedy_argmax
 from kavor_amd.utils.context import reset_context, set_context
 
 MAX_GRAPH_BATCH = 512
@@ -182,6 +186,8 @@ class ModelRunner:
         reserve_decode_workspace(max_bs, spec.num_attention_heads, spec.head_dim,
                                  self.max_blocks, self.block_size, self.device)
         self.logits_buf = torch.empty(max_bs, spec.vocab_size, dtype=torch.bfloat16, device=self.device)
+        self.sampled_buf = torch.zeros(max_bs, dtype=torch.int64, device=self.device)
+        argmax_workspace(self.device)
         self.graph_bs = graph_batch_sizes(max_bs)
         pool = None
         # all-zero metadata: context length 0 rows and slot 0 (model_runner.py:272-274)
@@ -191,11 +197,12 @@ class ModelRunner:
             set_context(False, slot_mapping=m.slot_mapping, context_lens=m.context_lens,
                         block_tables=m.block_tables)
             try:
-                out = self.logits_buf[:bs]
-                self.model.compute_logits(self.model(m.input_ids, m.positions), out=out)
+                out, tok = self.logits_buf[:bs], self.sampled_buf[:bs]
+                greedy_argmax(self.model.compute_logits(self.model(m.input_ids, m.positions), out=out), out=tok)
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, pool=pool):
-                    self.model.compute_logits(self.model(m.input_ids, m.positions), out=out)
+                    greedy_argmax(self.model.compute_logits(self.model(m.input_ids, m.positions), out=out),
+                                  out=tok)
             finally:
                 reset_context()
             if pool is None:
@@ -217,24 +224,27 @@ class ModelRunner:
                             m.slot_mapping, None, m.block_tables)
                 logits = self.model.compute_logits(self.model(m.input_ids, m.positions))
             else:
-                logits = self._decode(seqs)
+                logits, sampled = self._decode(seqs)
+                if all_greedy and sampled is not None:
+                    return sampled.tolist()  # the graph's LM head + greedy sampler
             t = None if all_greedy else torch.tensor(temps, dtype=torch.float32).to(self.device, non_blocking=True)
             return self.sampler(logits, t, all_greedy).tolist()
         finally:
             reset_context()
 
-    def _decode(self, seqs: list[Sequence]) -> torch.Tensor:
+    def _decode(self, seqs: list[Sequence]) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """Logits of a decode step, and the greedy tokens when a graph produced them."""
         n = len(seqs)
         if self.graphs and n <= self.graph_bs[-1]:
             bs = next(b for b in self.graph_bs if b >= n)
             self.staging.fill(seqs, self.block_size, bs)
             self.graphs[bs].replay()
-            return self.logits_buf[:n]
+            return self.logits_buf[:n], self.sampled_buf[:n]
         self.staging.fill(seqs, self.block_size, n)
         m = self.staging.views(n)
         set_context(False, slot_mapping=m.slot_mapping, context_lens=m.context_lens,
                     block_tables=m.block_tables)
-        return self.model.compute_logits(self.model(m.input_ids, m.positions))
+        return self.model.compute_logits(self.model(m.input_ids, m.positions)), None
 
     def exit(self) -> None:
         self.graphs.clear()

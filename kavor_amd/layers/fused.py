@@ -144,6 +144,26 @@ def silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torc
     return out
 
 
+_argmax_workspaces: dict[int, torch.Tensor] = {}
+# The largest split-row workspace any batch needs (fewer than 192 rows, up to 16 segments
+# of one 8-byte key each, at most 1024 keys); reserved once per device.
+_ARGMAX_WORKSPACE_BYTES = 16384
+
+
+def argmax_workspace(device: torch.device) -> torch.Tensor:
+    """The per-device workspace of the split-row argmax, allocated on first use (which the
+    engine makes before any graph capture)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _argmax_workspaces.get(index)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the argmax workspace must be reserved before graph capture: "
+                               "call argmax_workspace(device) first")
+        ws = torch.empty(_ARGMAX_WORKSPACE_BYTES, dtype=torch.uint8, device=torch.device("cuda", index))
+        _argmax_workspaces[index] = ws
+    return ws
+
+
 def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """int64 index of each row's maximum (first on ties, NaN largest)."""
     _check_bf16("logits", logits)
@@ -153,7 +173,11 @@ def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torc
         out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
     if out.dtype != torch.int64 or not out.is_contiguous() or out.numel() != logits.shape[0]:
         raise ValueError("out must be a contiguous int64 tensor with one entry per row")
+    ws = argmax_workspace(logits.device)
+    need = lib().kvp_argmax_workspace_bytes(logits.shape[0])
+    if need > ws.numel():
+        raise RuntimeError(f"argmax workspace of {ws.numel()} bytes, {need} needed")
     rc = lib().kvp_argmax_bf16(logits.data_ptr(), logits.stride(0), logits.shape[0], logits.shape[1],
-                               out.data_ptr(), _stream(logits))
+                               out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(logits))
     check("kvp_argmax_bf16", rc)
     return out

@@ -42,11 +42,18 @@ def graph_llm(cuda_device):
     llm.exit()
 
 
-def test_graph_decode_matches_reference(graph_llm):
+def test_graph_decode_matches_reference(graph_llm, monkeypatch):
+    """Greedy decode steps take their tokens from the graph's LM head + argmax: the
+    host-side sampler runs only for the prefill steps."""
+    runner = graph_llm.model_runner
+    calls = []
+    sampler = runner.sampler
+    monkeypatch.setattr(runner, "sampler", lambda *a: calls.append(1) or sampler(*a))
     prompts = _prompts(1, [1, 5, 63, 64, 65, 130, 300, 17, 200])
     sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True)
            for m in (12, 30, 7, 20, 64, 9, 25, 40, 3)]
     outs = graph_llm.generate(prompts, sps)
+    assert len(calls) == sum(s["prefill"] for s in graph_llm.step_stats)
     assert [len(o["token_ids"]) for o in outs] == [sp.max_tokens for sp in sps]
     assert graph_llm.model_runner.graphs, "decode graphs were not captured"
     assert any(not s["prefill"] for s in graph_llm.step_stats)

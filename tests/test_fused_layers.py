@@ -167,6 +167,38 @@ def test_greedy_argmax_screen_edge_cases(cuda_device):
     assert torch.equal(got, ref.greedy(rows))
 
 
+@pytest.mark.parametrize("rows", [1, 7, 100, 191, 192])
+def test_greedy_argmax_split_rows_equal_whole_rows(cuda_device, rows):
+    """Below 192 rows each row is split over several workgroups (up to 16 segments) whose
+    best (value, index) pairs are merged as ordered 64-bit keys.  The result must equal
+    the whole-row kernel (no workspace) and torch.argmax, with ties and NaNs placed
+    across segment boundaries and in the tail."""
+    from kavor_amd._lib import check, lib
+
+    V = 151936 + 5
+    g = torch.Generator().manual_seed(40 + rows)
+    logits = (torch.randn(rows, V, generator=g) * 3).to(torch.bfloat16)
+    logits[0, 9000] = logits[0, 150000] = 70.0          # tie across segments: first wins
+    if rows > 1:
+        logits[1, 151937] = 80.0                         # in the scalar tail
+    if rows > 2:
+        logits[2, 4] = float("nan")
+        logits[2, 120000] = float("nan")                 # first NaN wins
+        logits[3 % rows, :] = -0.0
+        logits[3 % rows, 60000] = 0.0                    # -0 == +0: index 0 wins
+    buf = torch.zeros(rows, V + 3, dtype=torch.bfloat16)
+    buf[:, :V] = logits
+    dev_logits = buf.to(cuda_device)[:, :V]
+    split = greedy_argmax(dev_logits).cpu()
+    whole = torch.empty(rows, dtype=torch.int64, device=cuda_device)
+    rc = lib().kvp_argmax_bf16(dev_logits.data_ptr(), dev_logits.stride(0), rows, V, whole.data_ptr(),
+                               None, 0, torch.cuda.current_stream(cuda_device).cuda_stream)
+    check("kvp_argmax_bf16", rc)
+    assert torch.equal(split, whole.cpu())
+    assert torch.equal(split, ref.greedy(logits))
+    assert split[0].item() == 9000
+
+
 @pytest.mark.parametrize("vocab", [1, 5, 8, 13])
 def test_greedy_argmax_tiny_vocab(cuda_device, vocab):
     g = torch.Generator().manual_seed(7 + vocab)
