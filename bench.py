@@ -113,6 +113,17 @@ def time_launches(fn, steps: int, warmup: int):
     return start.elapsed_time(end) / steps
 
 
+def warm_for(fn, seconds: float) -> None:
+    """Runs fn until `seconds` of wall time have passed (synchronising every 10 calls):
+    the clocks of a part that was idle take a few hundred milliseconds of full load to
+    settle, whatever the launch count."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_graph(fn, steps: int, warmup: int, per_graph: int = 20):
     """Average ms per call with `per_graph` calls captured in one graph and the graph
     replayed, for kernels shorter than the host's launch interval (eager launches of a
@@ -301,11 +312,12 @@ def bench_layers(dev, steps, warmup):
     return res
 
 
-def bench_prefill(dev, steps, warmup):
-    from kavor_amd.layers.attention import varlen_prefill
-    g = torch.Generator().manual_seed(0)
-    hq, hkv, nb = 16, 8, 4096
-    perm = torch.randperm(nb, generator=g).tolist()
+def prefill_workload(seed: int = 0):
+    """Config D's draws: 8 groups of 4 sequences, each group sharing a 256-aligned prefix
+    of 0-4096 tokens (identical leading block ids), each sequence 100-1024 new tokens in
+    its own blocks; returns (qlens, klens, tables) over a shuffled pool of 4096 blocks."""
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(4096, generator=g).tolist()
     qlens, klens, tables, pos = [], [], [], 0
     for _ in range(8):
         p = 256 * int(torch.randint(0, 17, (1,), generator=g))
@@ -318,19 +330,37 @@ def bench_prefill(dev, steps, warmup):
             qlens.append(n)
             klens.append(p + n)
             tables.append(shared + own)
+    return qlens, klens, tables
+
+
+def bench_prefill(dev, steps, warmup, dense: bool = False):
+    """Config D (paged, prefix-cached); with dense=True the same new tokens without their
+    prefixes, k / v given as packed [tokens, 8, 128] rows (the no-prefix batches of the
+    reference's caller, flash_attention_kvcache.py:76-79 with block_table None)."""
+    from kavor_amd.layers.attention import varlen_prefill
+    hq, hkv, nb = 16, 8, 4096
+    qlens, klens, tables = prefill_workload()
+    if dense:
+        klens = list(qlens)
     width = max(len(t) for t in tables)
     bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.int32, device=dev)
     cq = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0)), dtype=torch.int32, device=dev)
     ck = torch.tensor([0] + list(torch.tensor(klens).cumsum(0)), dtype=torch.int32, device=dev)
     dg = torch.Generator(device=dev).manual_seed(0)
-    kc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
-    vc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
     q = torch.randn(sum(qlens), hq, D, generator=dg, device=dev, dtype=torch.bfloat16)
+    if dense:
+        kc = torch.randn(sum(qlens), hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn(sum(qlens), hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+        bt = None
+    else:
+        kc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn(nb, BS, hkv, D, generator=dg, device=dev, dtype=torch.bfloat16)
     out = torch.empty_like(q)
 
     def step():
         varlen_prefill(q, kc, vc, max(qlens), cq, max(klens), ck, SCALE, causal=True, block_table=bt, out=out)
 
+    warm_for(step, 0.3)
     ms = time_launches(step, steps, warmup)
     flops = prefill_flops(cq.cpu().tolist(), ck.cpu().tolist(), hq, D)
     return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9)
@@ -344,6 +374,21 @@ def _median_runs(fn, budget_s: float, min_runs: int = 3, max_runs: int = 50) -> 
         fn()
         times.append(time.perf_counter() - t0)
     return statistics.median(times), len(times)
+
+
+def host_cpu() -> dict:
+    """The host the CPU baselines run on: threads torch uses (`cores`), the logical CPUs
+    the OS reports and the CPU model name."""
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(cores=torch.get_num_threads(), cpu_count=os.cpu_count(), cpu_model=model)
 
 
 def cpu_baseline_append(budget_s: float = 8.0):
@@ -360,7 +405,7 @@ def cpu_baseline_append(budget_s: float = 8.0):
                        torch.full((128,), -1, dtype=torch.int32)])
     sec, runs = _median_runs(lambda: torch_append(key, value, kc, vc, slots), budget_s)
     nbytes = append_bytes(slots.tolist(), hkv, D)
-    return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
+    return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", **host_cpu(), kind="port",
                 sample=f"whole workload (4096 tokens, 128 padding), torch {torch.__version__} index-put, "
                        f"median of {runs} runs")
 
@@ -370,21 +415,9 @@ def cpu_baseline_prefill(budget_s: float = 15.0, nseq: int = 4):
     first sequences of the prefix-cached prefill workload."""
     from oracle.kvpath_oracle import sdpa_varlen_prefill
 
-    g = torch.Generator().manual_seed(0)
-    hq, hkv, nb = 16, 8, 4096
-    perm = torch.randperm(nb, generator=g).tolist()
-    qlens, klens, tables, pos = [], [], [], 0
-    for _ in range(8):  # the same draws as bench_prefill
-        p = 256 * int(torch.randint(0, 17, (1,), generator=g))
-        shared = perm[pos:pos + p // BS]
-        pos += p // BS
-        for _ in range(4):
-            n = int(torch.randint(100, 1025, (1,), generator=g))
-            own = perm[pos:pos + math.ceil((p + n) / BS) - len(shared)]
-            pos += len(own)
-            qlens.append(n)
-            klens.append(p + n)
-            tables.append(shared + own)
+    hq, hkv = 16, 8
+    qlens, klens, tables = prefill_workload()  # the same draws as bench_prefill
+    g = torch.Generator().manual_seed(1)
     qlens, klens, tables = qlens[:nseq], klens[:nseq], tables[:nseq]
     ids = sorted({b for t in tables for b in t})
     remap = {b: i for i, b in enumerate(ids)}
@@ -397,7 +430,7 @@ def cpu_baseline_prefill(budget_s: float = 15.0, nseq: int = 4):
     ck = torch.tensor([0] + list(torch.tensor(klens).cumsum(0)), dtype=torch.int32)
     sec, runs = _median_runs(lambda: sdpa_varlen_prefill(q, kc, vc, cq, ck, SCALE, block_tables=bt), budget_s)
     flops = prefill_flops(cq.tolist(), ck.tolist(), hq, D)
-    return dict(value=round(flops / sec / 1e12, 4), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+    return dict(value=round(flops / sec / 1e12, 4), unit="TFLOP/s", **host_cpu(), kind="port",
                 sample=f"first {nseq} of 32 sequences ({sum(qlens)} query tokens, {sum(klens)} keys), "
                        f"torch {torch.__version__} bf16 SDPA with an explicit bottom-right mask, "
                        f"median of {runs} runs")
@@ -427,7 +460,7 @@ def cpu_baseline_decode(inp, budget_s: float = 20.0, nseq: int = 32):
             break
     sec = statistics.median(times)
     nbytes = decode_bytes(ctx.tolist(), inp["hq"], inp["hkv"], D, BS)
-    return dict(value=round(nbytes / sec / 1e9, 4), unit="GB/s", cores=torch.get_num_threads(),
+    return dict(value=round(nbytes / sec / 1e9, 4), unit="GB/s", **host_cpu(),
                 kind="port",
                 sample=f"first {nseq} of {inp['q'].shape[0]} sequences ({int(ctx.sum())} cached tokens), "
                        f"torch {torch.__version__} bf16 SDPA on {platform.processor() or platform.machine()}, "
@@ -494,7 +527,7 @@ def cpu_baseline_e2e(nseq: int = 16, steps: int = 3):
     for _ in range(steps):
         ids, ctx = decode_step(ids, ctx)
     sec = time.perf_counter() - t0
-    return dict(value=round(nseq * steps / sec, 2), unit="decode tok/s", cores=torch.get_num_threads(),
+    return dict(value=round(nseq * steps / sec, 2), unit="decode tok/s", **host_cpu(),
                 kind="port",
                 sample=f"{steps} greedy decode steps (after 1 warm-up) of the first {nseq} of 256 requests, "
                        f"engine weights, "
@@ -541,6 +574,12 @@ def run_extras(dev, steps: int, warmup: int, cpu_baseline: bool = False) -> dict
     extras["varlen_prefill"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
                                     ms=round(p["ms"], 4), flops=p["flops"],
                                     workload="32 seqs, new 100-1024, prefix 0-4096 shared by groups of 4, 16q/8kv")
+    torch.cuda.empty_cache()
+    p = bench_prefill(dev, *n["prefill"], dense=True)
+    extras["varlen_prefill_dense"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                          ms=round(p["ms"], 4), flops=p["flops"],
+                                          workload="config D's 32 sequences of 100-1024 new tokens without "
+                                                   "prefixes, dense k/v rows (block_table None), 16q/8kv")
     torch.cuda.empty_cache()
     extras["layer_kernels"] = bench_layers(dev, *n["layers"])
     torch.cuda.empty_cache()
@@ -779,12 +818,16 @@ E2E_PROFILE_CMDS = [
     "cd /tmp && export TMPDIR=/tmp",
     "rocprofv3 --kernel-trace --stats --output-format csv -d $OUT/e2e_trace -o run -- python $R/bench.py --e2e-only",
     "python $R/bench.py --summarize-e2e $OUT/e2e_trace",
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $OUT/e2e_dropin -o run -- python $R/bench.py --e2e-only "
+    "--e2e-caller dropin",
+    "python $R/bench.py --summarize-e2e $OUT/e2e_dropin dropin",
 ]
 
 
-def summarize_e2e(trace_dir: str) -> int:
-    """profiles/e2e_qwen3_0.6b.md: where the end-to-end generation spends GPU time, from
-    the --stats output of rocprofv3 over `bench.py --e2e-only`."""
+def summarize_e2e(trace_dir: str, caller: str = "fused") -> int:
+    """profiles/e2e_qwen3_0.6b.md (fused caller) or profiles/e2e_qwen3_0.6b_dropin.md:
+    where the end-to-end generation spends GPU time, from the --stats output of rocprofv3
+    over `bench.py --e2e-only [--e2e-caller dropin]`."""
     import csv
 
     with open(Path(trace_dir) / "run_kernel_stats.csv") as f:
@@ -803,7 +846,8 @@ def summarize_e2e(trace_dir: str) -> int:
         g = group(r["Name"])
         t, c = by.get(g, (0.0, 0))
         by[g] = (t + float(r["TotalDurationNs"]), c + int(r["Calls"]))
-    lines = ["# e2e_qwen3_0.6b: GPU time of the end-to-end generation, by kernel", "",
+    title = "e2e_qwen3_0.6b" + ("" if caller == "fused" else "_" + caller)
+    lines = [f"# {title}: GPU time of the end-to-end generation ({caller} attention caller), by kernel", "",
              "Commands (from the repository root on the GPU host, `R=$PWD`, `OUT` a directory for the raw results):", "", "```"]
     lines += E2E_PROFILE_CMDS + ["```", "",
                                  f"Total kernel time {total / 1e9:.3f} s (profiler overhead included; the "
@@ -811,7 +855,7 @@ def summarize_e2e(trace_dir: str) -> int:
                                  "| kernel | calls | total s | share | avg us |", "|---|---|---|---|---|"]
     for g, (t, c) in sorted(by.items(), key=lambda x: -x[1][0]):
         lines.append(f"| `{g}` | {c} | {t / 1e9:.3f} | {100 * t / total:.1f}% | {t / c / 1e3:.2f} |")
-    out = ROOT / "profiles" / "e2e_qwen3_0.6b.md"
+    out = ROOT / "profiles" / f"{title}.md"
     out.write_text("\n".join(lines) + "\n")
     print(f"wrote {out}", flush=True)
     return 0
@@ -848,14 +892,16 @@ def e2e_workload(num_seqs: int = 256, seed: int = 0):
     return prompts, max_tokens
 
 
-def bench_e2e(num_seqs: int = 256):
+def bench_e2e(num_seqs: int = 256, caller: str = "fused"):
     """Offline generation with the Qwen3-0.6B architecture (random bf16 weights), greedy,
-    ignore_eos, hipGraph decode, max_model_len 4096: output tok/s = sum(max_tokens) / wall."""
+    ignore_eos, hipGraph decode, max_model_len 4096: output tok/s = sum(max_tokens) / wall.
+    caller "dropin" runs the layers in the reference's order (q/k norm + RoPE, then
+    Attention.forward appending through store_kvcache, dense prefill without a prefix)."""
     from kavor_amd.engine.llm_engine import LLM
     from kavor_amd.sampling_params import SamplingParams
 
     t0 = time.perf_counter()
-    llm = LLM(None, enforce_eager=False, max_model_len=4096, seed=0)
+    llm = LLM(None, enforce_eager=False, max_model_len=4096, seed=0, attention_caller=caller)
     init_s = time.perf_counter() - t0
     print(f"e2e: engine ready in {init_s:.1f}s ({llm.config.num_kvcache_blocks} pages, "
           f"{len(llm.model_runner.graphs)} graphs)", file=sys.stderr, flush=True)
@@ -882,7 +928,7 @@ def bench_e2e(num_seqs: int = 256):
         init_s=round(init_s, 2), capture_s=round(runner.timings["capture"], 2),
         workload=f"{num_seqs} requests, prompt U[100,1024] ids uniform over 151936, output U[100,1024], "
                  "greedy, ignore_eos, Qwen3-0.6B arch random bf16 weights, max_model_len 4096, "
-                 "hipGraph decode, block 256",
+                 f"hipGraph decode, block 256, {caller} attention caller",
     )
     llm.exit()
     del llm
@@ -1021,6 +1067,8 @@ def main() -> int:
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen3-0.6B generation")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end generation (prints its JSON)")
     ap.add_argument("--e2e-seqs", type=int, default=256)
+    ap.add_argument("--e2e-caller", choices=("fused", "dropin"), default="fused",
+                    help="layer order of --e2e-only: the fused q/k kernel, or the reference's caller order")
     ap.add_argument("--summarize", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/*.md (and the decode traffic json) from the CSV output of "
                          "three rocprofv3 runs of --profile: --kernel-trace --stats, --pmc "
@@ -1033,13 +1081,13 @@ def main() -> int:
                     help="only the prefix-cached prefill launches (30), for rocprofv3 --pmc passes")
     ap.add_argument("--summarize-prefill-pmc", nargs=2, metavar=("PASS_A_DIR", "PASS_B_DIR"),
                     help="write profiles/varlen_prefill_prefix_32seq_pmc.md from the two --pmc passes")
-    ap.add_argument("--summarize-e2e", metavar="TRACE_DIR",
+    ap.add_argument("--summarize-e2e", nargs="+", metavar="TRACE_DIR [CALLER]",
                     help="write profiles/e2e_qwen3_0.6b.md from rocprofv3 --stats over --e2e-only")
     args = ap.parse_args()
     if args.summarize:
         return summarize_profiles(*args.summarize)
     if args.summarize_e2e:
-        return summarize_e2e(args.summarize_e2e)
+        return summarize_e2e(*args.summarize_e2e)
     if args.summarize_prefill_pmc:
         return summarize_prefill_pmc(*args.summarize_prefill_pmc)
     if args.gpus != 1:
@@ -1061,7 +1109,7 @@ def main() -> int:
         print("prefill profile run done", flush=True)
         return 0
     if args.e2e_only:
-        print(json.dumps({"e2e_qwen3_0.6b": bench_e2e(args.e2e_seqs)}), flush=True)
+        print(json.dumps({"e2e_qwen3_0.6b": bench_e2e(args.e2e_seqs, args.e2e_caller)}), flush=True)
         return 0
 
     # The headline is timed first: after the extra workloads (seconds of full-power GPU
@@ -1078,6 +1126,9 @@ def main() -> int:
         del inp
         torch.cuda.empty_cache()
         extras["e2e_qwen3_0.6b"] = bench_e2e(args.e2e_seqs)
+        d = bench_e2e(args.e2e_seqs, caller="dropin")
+        extras["e2e_qwen3_0.6b"]["dropin"] = {k: d[k] for k in ("output_tok_s", "decode_tok_s", "wall_s",
+                                                               "prefill_tok_s", "workload")}
         extras["e2e_qwen3_0.6b"]["reference_design"] = bench_e2e_window()
         if not args.no_cpu_baseline:
             extras["e2e_qwen3_0.6b"]["cpu_baseline"] = cpu_baseline_e2e()

@@ -230,6 +230,23 @@ int kvp_qk_norm_rope_append_bf16(const void* qkv, int64_t qkv_tok_stride,
                                  int32_t block_size, void* stream);
 
 /*
+ * The same per-token q/k RMSNorm + neox RoPE without the append: q goes to q_out as
+ * above and k to k_out + t*k_out_tok_stride + h*128 (a fresh [tokens, num_kv_heads, 128]
+ * tensor); the v heads of qkv are not read.  Replaces q_norm, k_norm and rotary_emb
+ * (kavor/models/qwen3.py:85-88; layernorm.py:8-40; rotary_embedding.py:8-53) for a
+ * caller that then passes q, k and the v view of qkv to Attention.forward, which appends
+ * k and v itself (flash_attention_kvcache.py:71-72).  qkv's row stride must cover the
+ * q and k heads.
+ */
+int kvp_qk_norm_rope_bf16(const void* qkv, int64_t qkv_tok_stride,
+                          const int32_t* positions, const float* cos_sin, int32_t max_position,
+                          const void* q_norm_weight, const void* k_norm_weight, float eps,
+                          void* q_out, int64_t q_out_tok_stride,
+                          void* k_out, int64_t k_out_tok_stride,
+                          int32_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                          int32_t head_dim, void* stream);
+
+/*
  * out[t, i] = bf16(silu(gate[t, i]) * up[t, i]) with gate = gate_up[t, 0:intermediate],
  * up = gate_up[t, intermediate:2*intermediate], computed in fp32 and rounded once
  * (SiluAndMul, kavor/layers/activation.py:6-11, under torch.compile).  intermediate is a

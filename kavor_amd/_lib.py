@@ -93,6 +93,15 @@ SIGNATURES: dict[str, tuple] = {
         _i32, _i32, _i32, _i32,           # num_q_heads, num_kv_heads, head_dim, block_size
         _c_void_p,                        # stream
     ]),
+    "kvp_qk_norm_rope_bf16": (ctypes.c_int, [
+        _c_void_p, _i64,                  # qkv, qkv_tok_stride
+        _c_void_p, _c_void_p, _i32,       # positions, cos_sin, max_position
+        _c_void_p, _c_void_p, _f32,       # q_norm_weight, k_norm_weight, eps
+        _c_void_p, _i64,                  # q_out, q_out_tok_stride
+        _c_void_p, _i64,                  # k_out, k_out_tok_stride
+        _i32, _i32, _i32, _i32,           # num_tokens, num_q_heads, num_kv_heads, head_dim
+        _c_void_p,                        # stream
+    ]),
     "kvp_silu_mul_bf16": (ctypes.c_int, [
         _c_void_p, _i64, _c_void_p, _i64,  # gate_up, gate_up_tok_stride, out, out_tok_stride
         _i32, _i32, _c_void_p,            # num_tokens, intermediate, stream

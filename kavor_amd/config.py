@@ -8,7 +8,12 @@ weights are random (seeded by `seed`).  Differences from the reference:
 - kvcache_block_size must be a multiple of 64 (the page size the HIP kernels tile by;
   the reference requires multiples of 256 because flash-attn does, config.py:42);
 - num_kvcache_blocks > 0 fixes the page-pool size instead of sizing it from
-  gpu_memory_utilization.
+  gpu_memory_utilization;
+- attention_caller picks how the Qwen3 layers call the paged path: "fused" (one kernel
+  normalises, rotates and appends k / v, then attention reads the pages) or "dropin"
+  (the reference's order, kavor/models/qwen3.py:85-90: q/k norm + RoPE, then
+  Attention.forward(q, k, v) appends through store_kvcache and runs dense varlen
+  prefill for batches without a cached prefix).
 """
 
 from __future__ import annotations
@@ -33,6 +38,7 @@ class Config:
     kvcache_block_size: int = 256
     num_kvcache_blocks: int = -1
     seed: int = 0
+    attention_caller: str = "fused"
     spec: Qwen3Spec = field(init=False)
     checkpoint: str | None = field(init=False, default=None)
 
@@ -51,6 +57,8 @@ class Config:
         if self.kvcache_block_size % 64 != 0 or self.kvcache_block_size <= 0:
             raise ValueError(f"kvcache_block_size must be a positive multiple of 64, "
                              f"got {self.kvcache_block_size}")
+        if self.attention_caller not in ("fused", "dropin"):
+            raise ValueError(f"attention_caller must be 'fused' or 'dropin', got {self.attention_caller!r}")
         if not 0.0 < self.gpu_memory_utilization <= 1.0:
             raise ValueError("gpu_memory_utilization must be in (0, 1]")
         if self.max_num_seqs < 1 or self.max_num_batched_tokens < 1:

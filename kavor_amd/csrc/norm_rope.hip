@@ -142,7 +142,10 @@ struct QkParams {
   uint16_t* v_cache;
   int64_t blk_stride, slot_stride, head_stride, num_cache_slots;
   const int32_t* slot_mapping;
+  uint16_t* k_out;             // non-null: k goes here ([token][hkv][D]), not into the pages
+  int64_t k_out_stride;        // token stride of k_out; heads D apart
   int num_tokens, hq, hkv, block_size;
+  int rows;                    // head rows per token: hq + 2 hkv, or hq + hkv without v
 };
 
 // A token's hq + 2 hkv head rows ([0, hq) q, [hq, hq+hkv) k, [hq+hkv, hq+2hkv) v) are
@@ -189,7 +192,7 @@ template <int NB>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(QkParams p) {
   const int lane = threadIdx.x & 63;
   const int r = lane >> 4, j = lane & 15;
-  const int heads = p.hq + 2 * p.hkv;
+  const int heads = p.rows;
   const int groups = (heads + 4 * NB - 1) / (4 * NB);  // waves per token
   const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   const int t = wave / groups;
@@ -239,12 +242,13 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(QkParams 
       continue;
     }
     const bool is_q = h < p.hq;
-    if (!is_q && !store_kv) continue;  // k head of a padding token
+    if (!is_q && !store_kv && !p.k_out) continue;  // k head of a padding token
     float x[8];
     unpack8(raw[u], x);
     norm_rope_head(x, is_q ? wq : wk, c, sn, first_half, pos_ok, p.eps);
     const uint4 packed = pack8(x);
     if (is_q) store16(p.q_out + t * p.q_out_stride + h * kRopeDim + 8 * j, packed);
+    else if (p.k_out) store16(p.k_out + t * p.k_out_stride + (h - p.hq) * kRopeDim + 8 * j, packed);
     else store16(p.k_cache + cache_off + (h - p.hq) * p.head_stride, packed);
   }
 }
@@ -461,6 +465,22 @@ extern "C" int kvp_rmsnorm_bf16(const void* x, int64_t x_stride0, int64_t x_stri
   return launch_status("rmsnorm_kernel");
 }
 
+// Prefill-sized inputs: 4 head rows per 16-lane row (two waves per token for Qwen3);
+// decode-sized ones: one head row per 16-lane row, several waves per token.
+static int launch_qk(const QkParams& p, hipStream_t s) {
+  const bool wide = p.num_tokens >= kQkWideTokens;
+  const int nb = wide ? 4 : 1;
+  const int64_t groups = (p.rows + 4 * nb - 1) / (4 * nb);
+  const int64_t waves = static_cast<int64_t>(p.num_tokens) * groups;
+  const int64_t grid = (waves + kThreads / 64 - 1) / (kThreads / 64);
+  if (grid > INT32_MAX) return fail(KVP_EINVAL, "too many tokens");
+  if (wide)
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel<1>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, p);
+  return launch_status("qk_norm_rope_append_kernel");
+}
+
 extern "C" int kvp_qk_norm_rope_append_bf16(
     const void* qkv, int64_t qkv_tok_stride, const int32_t* positions, const float* cos_sin,
     int32_t max_position, const void* q_norm_weight, const void* k_norm_weight, float eps,
@@ -490,27 +510,44 @@ extern "C" int kvp_qk_norm_rope_append_bf16(
     return fail(KVP_EINVAL, "qkv row stride %lld is shorter than (hq + 2 hkv) * head_dim",
                 (long long)qkv_tok_stride);
   if (num_tokens == 0) return KVP_OK;
-  // Prefill-sized inputs: 4 head rows per 16-lane row (two waves per token for Qwen3);
-  // decode-sized ones: one head row per 16-lane row, several waves per token.
-  const bool wide = num_tokens >= kQkWideTokens;
-  const int nb = wide ? 4 : 1;
-  const int64_t groups = (num_q_heads + 2 * num_kv_heads + 4 * nb - 1) / (4 * nb);
-  const int64_t waves = static_cast<int64_t>(num_tokens) * groups;
-  const int64_t grid = (waves + kThreads / 64 - 1) / (kThreads / 64);
-  if (grid > INT32_MAX) return fail(KVP_EINVAL, "too many tokens");
   QkParams p{static_cast<const uint16_t*>(qkv), qkv_tok_stride, positions, cos_sin, max_position,
              static_cast<const uint16_t*>(q_norm_weight), static_cast<const uint16_t*>(k_norm_weight),
              eps, static_cast<uint16_t*>(q_out), q_out_tok_stride,
              static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
              cache_block_stride, cache_slot_stride, cache_head_stride, num_cache_slots,
-             slot_mapping, num_tokens, num_q_heads, num_kv_heads, block_size};
-  if (wide)
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
-                       static_cast<hipStream_t>(stream), p);
-  else
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel<1>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
-                       static_cast<hipStream_t>(stream), p);
-  return launch_status("qk_norm_rope_append_kernel");
+             slot_mapping, nullptr, 0, num_tokens, num_q_heads, num_kv_heads, block_size,
+             num_q_heads + 2 * num_kv_heads};
+  return launch_qk(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvp_qk_norm_rope_bf16(const void* qkv, int64_t qkv_tok_stride, const int32_t* positions,
+                                     const float* cos_sin, int32_t max_position, const void* q_norm_weight,
+                                     const void* k_norm_weight, float eps, void* q_out,
+                                     int64_t q_out_tok_stride, void* k_out, int64_t k_out_tok_stride,
+                                     int32_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, void* stream) {
+  clear_error();
+  if (head_dim != kRopeDim)
+    return fail(KVP_EUNSUPPORTED, "head_dim=%d: the q/k norm + RoPE kernel handles 128", head_dim);
+  if (!qkv || !positions || !cos_sin || !q_norm_weight || !k_norm_weight || !q_out || !k_out)
+    return fail(KVP_EINVAL, "null pointer");
+  if (num_tokens < 0 || num_q_heads < 1 || num_kv_heads < 1 || max_position < 1)
+    return fail(KVP_EINVAL, "bad shape");
+  if (!aligned16(qkv) || !aligned16(q_out) || !aligned16(k_out) || !aligned16(cos_sin) ||
+      !aligned16(q_norm_weight) || !aligned16(k_norm_weight))
+    return fail(KVP_EINVAL, "pointers must be 16-byte aligned");
+  if (!mult8(qkv_tok_stride) || !mult8(q_out_tok_stride) || !mult8(k_out_tok_stride))
+    return fail(KVP_EINVAL, "strides must be multiples of 8 elements");
+  if (qkv_tok_stride < static_cast<int64_t>(num_q_heads + num_kv_heads) * head_dim)
+    return fail(KVP_EINVAL, "qkv row stride %lld is shorter than (hq + hkv) * head_dim",
+                (long long)qkv_tok_stride);
+  if (num_tokens == 0) return KVP_OK;
+  QkParams p{static_cast<const uint16_t*>(qkv), qkv_tok_stride, positions, cos_sin, max_position,
+             static_cast<const uint16_t*>(q_norm_weight), static_cast<const uint16_t*>(k_norm_weight),
+             eps, static_cast<uint16_t*>(q_out), q_out_tok_stride, nullptr, nullptr, 0, 0, 0, 0,
+             nullptr, static_cast<uint16_t*>(k_out), k_out_tok_stride, num_tokens, num_q_heads, num_kv_heads,
+             1, num_q_heads + num_kv_heads};
+  return launch_qk(p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int kvp_silu_mul_bf16(const void* gate_up, int64_t gate_up_tok_stride, void* out,

@@ -18,9 +18,10 @@ the shared-memory control plane of :85-106 has nothing to do):
 - run / run_model (:213-262): prefill runs eagerly, decode replays the smallest graph
   that holds the batch, padding rows carry slot -1 and context length 0.
 
-Per-step metadata travels in one host-to-device copy (kavor_amd.engine.metadata); the
-prefill always carries block tables because the model appends k / v before attention
-and attention reads the pages.  An all-greedy decode batch reads its tokens from the
+Per-step metadata travels in one host-to-device copy (kavor_amd.engine.metadata).  With
+the fused layers the prefill always carries block tables, because the model appends
+k / v before attention and attention reads the pages; with the drop-in caller order it
+carries them only when some sequence has cached tokens (:432-433).  An all-greedy decode batch reads its tokens from the
 graph's sampled_tokens; a batch with a temperature above 0 samples from the graph's
 logits after the replay (the reference's graph samples every temperature inside).
 """
@@ -67,7 +68,7 @@ class ModelRunner:
         self.timings = {"load": 0.0, "pool": 0.0, "capture": 0.0}
 
         t0 = perf_counter()
-        self.model = Qwen3ForCausalLM(self.spec, self.device)
+        self.model = Qwen3ForCausalLM(self.spec, self.device, caller=config.attention_caller)
         if config.checkpoint is not None:
             tensors = load_checkpoint_tensors(config.checkpoint)
             self.model.load_hf_state({k: v.to(self.device) for k, v in tensors.items()})
@@ -111,7 +112,8 @@ class ModelRunner:
         tables = torch.arange(num_seqs * nb, dtype=torch.int32, device=dev).view(num_seqs, nb)
         slots = (tables[:, p // self.block_size] * self.block_size + p % self.block_size).reshape(-1)
         cu = torch.arange(0, total + 1, seq_len, dtype=torch.int32, device=dev)
-        set_context(True, cu, cu, seq_len, seq_len, slots.contiguous(), None, tables)
+        set_context(True, cu, cu, seq_len, seq_len, slots.contiguous(), None,
+                    tables if self.model.prefill_reads_pages else None)
         try:
             logits = self.model.compute_logits(self.model(ids, pos))
             self.sampler(logits, None, True)
@@ -219,7 +221,8 @@ class ModelRunner:
         all_greedy = all(t == 0.0 for t in temps)
         try:
             if is_prefill:
-                m = prepare_prefill(seqs, self.block_size, self.device, always_tables=True)
+                m = prepare_prefill(seqs, self.block_size, self.device,
+                                    always_tables=self.model.prefill_reads_pages)
                 set_context(True, m.cu_seqlens_q, m.cu_seqlens_k, m.max_seqlen_q, m.max_seqlen_k,
                             m.slot_mapping, None, m.block_tables)
                 logits = self.model.compute_logits(self.model(m.input_ids, m.positions))

@@ -6,14 +6,19 @@ The model is the caller of the path (kavor/models/qwen3.py:75-91).  Per layer:
   -> paged attention over the page pool (HIP) -> o GEMM -> add-RMSNorm (HIP)
   -> gate_up GEMM -> SiLU * up (HIP) -> down GEMM
 
+With caller="dropin" the attention block keeps the reference's order instead: q/k
+RMSNorm + RoPE (HIP, k into a fresh tensor), then Attention.forward(q, k, v) with v a
+view of the qkv rows, which appends k / v (store_kvcache) and runs varlen prefill
+(dense, or paged when the batch has cached prefixes) or paged decode.
+
 GEMMs are torch (hipBLASLt); every other op is a kernel of libkvpath.so
 (kavor_amd.layers.fused, kavor_amd.layers.attention), with the reference's numerics:
 RMSNorm statistics in fp32 and the normalised value rounded to bf16 before the weight
 (kavor/layers/layernorm.py:235-284), neox RoPE in fp32 (rotary_embedding.py:8-53), SiLU in
 fp32 (activation.py:6-11).  Because k and v go straight from the qkv rows into the
-pages, prefill attention always reads the pages (the runner always passes block
-tables), which is the reference's prefix-cache mode (flash_attention_kvcache.py:74-79)
-applied to every prefill.  The embedding / LM head are tied; during prefill only each
+pages, prefill attention always reads the pages in the fused order (the runner always
+passes block tables), which is the reference's prefix-cache mode
+(flash_attention_kvcache.py:74-79) applied to every prefill.  The embedding / LM head are tied; during prefill only each
 sequence's last token is projected to logits (kavor/layers/embed_head.py:56-66).
 """
 
@@ -112,8 +117,9 @@ def _weight(*shape, device, dtype) -> nn.Parameter:
 
 class Qwen3Attention(nn.Module):
 
-    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype):
+    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype, caller: str = "fused"):
         super().__init__()
+        self.caller = caller
         self.num_heads = spec.num_attention_heads
         self.num_kv_heads = spec.num_key_value_heads
         self.head_dim = spec.head_dim
@@ -128,6 +134,8 @@ class Qwen3Attention(nn.Module):
 
     def forward(self, positions: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
         qkv = F.linear(hidden, self.qkv_proj)
+        if self.caller == "dropin":
+            return self.forward_dropin(positions, qkv)
         attn = self.attn
         k_cache, v_cache = attn.k_cache[0], attn.v_cache[0]
         bound = k_cache.numel() > 0 and v_cache.numel() > 0
@@ -137,6 +145,17 @@ class Qwen3Attention(nn.Module):
             get_context().slot_mapping if bound else None)
         o = attn.forward_cached(q)
         return F.linear(o.reshape(q.shape[0], self.q_size), self.o_proj)
+
+    def forward_dropin(self, positions: torch.Tensor, qkv: torch.Tensor) -> torch.Tensor:
+        """The reference's caller order (kavor/models/qwen3.py:80-90): q_norm, k_norm and
+        rotary_emb (one HIP launch; k comes out contiguous with row stride Hkv*D), v a
+        strided view of the qkv rows (row stride (Hq+2Hkv)*D), then attn(q, k, v)."""
+        T = qkv.shape[0]
+        q, k = fused.qk_norm_rope(qkv, positions, self.rope, self.q_norm.weight, self.k_norm.weight,
+                                  self.q_norm.eps, self.num_heads, self.num_kv_heads)
+        v = qkv[:, self.q_size + self.kv_size:].view(T, self.num_kv_heads, self.head_dim)
+        o = self.attn(q, k, v)
+        return F.linear(o.reshape(T, self.q_size), self.o_proj)
 
 
 class Qwen3MLP(nn.Module):
@@ -153,9 +172,9 @@ class Qwen3MLP(nn.Module):
 
 class Qwen3DecoderLayer(nn.Module):
 
-    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype):
+    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype, caller: str = "fused"):
         super().__init__()
-        self.self_attn = Qwen3Attention(spec, rope, device, dtype)
+        self.self_attn = Qwen3Attention(spec, rope, device, dtype, caller)
         self.mlp = Qwen3MLP(spec, device, dtype)
         self.input_layernorm = RMSNorm(spec.hidden_size, spec.rms_norm_eps, device, dtype)
         self.post_attention_layernorm = RMSNorm(spec.hidden_size, spec.rms_norm_eps, device, dtype)
@@ -173,14 +192,18 @@ class Qwen3DecoderLayer(nn.Module):
 class Qwen3ForCausalLM(nn.Module):
     """Qwen3 causal LM over the paged KV cache (bf16 weights on one GPU)."""
 
-    def __init__(self, spec: Qwen3Spec, device, dtype=torch.bfloat16):
+    def __init__(self, spec: Qwen3Spec, device, dtype=torch.bfloat16, caller: str = "fused"):
         super().__init__()
         self.spec = spec
+        # prefill attention reads the pages (block tables on every prefill) when the layers
+        # append k / v before attention; the drop-in order attends over fresh k / v unless
+        # a prefix is cached
+        self.prefill_reads_pages = caller == "fused"
         rope = rope_cache(spec.head_dim, spec.max_position_embeddings, spec.rope_theta, device)
         self.register_buffer("rope_table", rope, persistent=False)
         self.embed_tokens = _weight(spec.vocab_size, spec.hidden_size, device=device, dtype=dtype)
         self.layers = nn.ModuleList(
-            [Qwen3DecoderLayer(spec, rope, device, dtype) for _ in range(spec.num_hidden_layers)])
+            [Qwen3DecoderLayer(spec, rope, device, dtype, caller) for _ in range(spec.num_hidden_layers)])
         self.norm = RMSNorm(spec.hidden_size, spec.rms_norm_eps, device, dtype)
         self.lm_head = (self.embed_tokens if spec.tie_word_embeddings
                         else _weight(spec.vocab_size, spec.hidden_size, device=device, dtype=dtype))

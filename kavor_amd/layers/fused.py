@@ -3,6 +3,7 @@
 These replace the engine-side Triton kernels around the paged KV path:
   rms_norm / add_rms_norm   kavor/layers/layernorm.py:235-284 (RMSNorm.forward)
   qk_norm_rope_append       q_norm + k_norm + rotary_emb + store_kvcache of qwen3.py:85-89
+  qk_norm_rope              q_norm + k_norm + rotary_emb of qwen3.py:85-88 (no append)
   silu_and_mul              kavor/layers/activation.py:6-11
   greedy_argmax             the temperature-0 path of kavor/layers/sampler.py:7-66
 Each function only validates layouts and forwards pointers and strides to the C ABI on
@@ -15,7 +16,8 @@ import torch
 
 from kavor_amd._lib import check, lib
 
-__all__ = ["rms_norm", "add_rms_norm", "qk_norm_rope_append", "silu_and_mul", "greedy_argmax"]
+__all__ = ["rms_norm", "add_rms_norm", "qk_norm_rope_append", "qk_norm_rope", "silu_and_mul",
+           "greedy_argmax"]
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -125,6 +127,38 @@ def qk_norm_rope_append(qkv: torch.Tensor, positions: torch.Tensor, cos_sin: tor
         block_size, _stream(qkv))
     check("kvp_qk_norm_rope_append_bf16", rc)
     return q_out
+
+
+def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, cos_sin: torch.Tensor,
+                 q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
+                 num_q_heads: int, num_kv_heads: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """q/k RMSNorm + neox RoPE of the fused qkv rows without the append: returns fresh
+    q [T, Hq, 128] and k [T, Hkv, 128] (the q_norm, k_norm and rotary_emb of
+    kavor/models/qwen3.py:85-88, one launch); v stays a view of qkv."""
+    _check_bf16("qkv", qkv)
+    if qkv.dim() != 2:
+        raise ValueError("qkv must be [num_tokens, (Hq + 2 Hkv) * head_dim]")
+    T = qkv.shape[0]
+    D = cos_sin.shape[1]
+    if qkv.shape[1] < (num_q_heads + num_kv_heads) * D:
+        raise ValueError("qkv is narrower than the q and k heads")
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.dim() != 2:
+        raise ValueError("cos_sin must be a contiguous fp32 [max_position, head_dim] table")
+    if positions.dtype != torch.int32 or not positions.is_contiguous() or positions.numel() != T:
+        raise ValueError("positions must be a contiguous int32 tensor with one entry per token")
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        _check_bf16(name, w)
+        if w.shape != (D,):
+            raise ValueError(f"{name} must have head_dim elements")
+    q = torch.empty(T, num_q_heads, D, dtype=torch.bfloat16, device=qkv.device)
+    k = torch.empty(T, num_kv_heads, D, dtype=torch.bfloat16, device=qkv.device)
+    rc = lib().kvp_qk_norm_rope_bf16(
+        qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0],
+        q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(eps),
+        q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), T, num_q_heads, num_kv_heads, D,
+        _stream(qkv))
+    check("kvp_qk_norm_rope_bf16", rc)
+    return q, k
 
 
 def silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -164,3 +164,39 @@ def test_reference_design_comparator_is_correct(cuda_device, monkeypatch):
         _check(llm, prompts, outs)
     finally:
         llm.exit()
+
+
+def test_dropin_caller_order_matches_reference(cuda_device, monkeypatch):
+    """The reference's caller order (q/k norm + RoPE, then Attention.forward(q, k, v),
+    which appends through store_kvcache): batches without a cached prefix run the dense
+    varlen prefill over the fresh k / v, a batch with a prefix hit reads the pages, and
+    decode replays graphs whose layers call the append kernel and the paged decode."""
+    from kavor_amd.layers import attention
+
+    modes, appends = [], []
+    prefill, store = attention.varlen_prefill, attention.store_kvcache
+    monkeypatch.setattr(attention, "varlen_prefill",
+                        lambda *a, **kw: modes.append(kw.get("block_table") is not None) or prefill(*a, **kw))
+    monkeypatch.setattr(attention, "store_kvcache", lambda *a: appends.append(a[0].shape[0]) or store(*a))
+    llm = LLM(TINY, kvcache_block_size=64, max_model_len=1024, num_kvcache_blocks=128,
+              max_num_seqs=8, max_num_batched_tokens=512, attention_caller="dropin", seed=0)
+    try:
+        assert llm.model_runner.graphs
+        modes.clear()   # drop the warm-up and capture calls
+        appends.clear()
+        base = _prompts(11, [200])[0]
+        first = [base, _prompts(12, [90])[0], _prompts(13, [600])[0]]   # 600 > budget: chunked
+        sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True) for m in (20, 33, 9)]
+        outs = llm.generate(first, sps)
+        assert False in modes and True in modes  # dense first step, paged second chunk
+        n_dense = modes.count(False)
+        second = [base + [3, 4], _prompts(14, [70])[0]]   # mixed batch: one prefix hit
+        outs2 = llm.generate(second, SamplingParams(temperature=0.0, max_tokens=12, ignore_eos=True))
+        assert llm.scheduler.block_manager.prefix_cache_hit_tokens >= 192
+        assert modes.count(False) == n_dense  # the mixed batch read the pages
+        assert min(appends) >= 1
+        _check(llm, first, outs)
+        _check(llm, second, outs2)
+    finally:
+        llm.exit()
+

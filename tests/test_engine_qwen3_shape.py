@@ -59,10 +59,14 @@ def _requests():
     return prompts, max_tokens
 
 
-@pytest.fixture(scope="module")
-def llm(cuda_device):
+@pytest.fixture(scope="module", params=["fused", "dropin"])
+def llm(cuda_device, request):
+    """Both caller orders: the fused q/k norm + RoPE + append kernel before attention over
+    the pages, and the reference's order (Attention.forward appends, then dense or paged
+    prefill)."""
     engine = LLM(SPEC, kvcache_block_size=BLOCK, max_model_len=4096, max_num_seqs=8,
-                 max_num_batched_tokens=BUDGET, gpu_memory_utilization=0.5, seed=0)
+                 max_num_batched_tokens=BUDGET, gpu_memory_utilization=0.5, seed=0,
+                 attention_caller=request.param)
     yield engine
     engine.exit()
     torch.cuda.empty_cache()

@@ -100,6 +100,37 @@ def test_qk_norm_rope_append(cuda_device, T, hq, hkv):
     torch.testing.assert_close(kc_h[mask].float(), want_k[mask].float(), **TOL)
 
 
+@pytest.mark.parametrize("T,hq,hkv", [(1, 16, 8), (300, 16, 8), (2050, 32, 8), (7, 5, 1)])
+def test_qk_norm_rope_k_out(cuda_device, T, hq, hkv):
+    """The no-append variant: q and k come out as fresh tensors (k contiguous, Hkv heads),
+    v is not read (NaN-filled v heads must not leak), and nothing else is written."""
+    from kavor_amd.layers.fused import qk_norm_rope
+
+    D, max_pos = 128, 4096
+    g = torch.Generator().manual_seed(12)
+    qkv = _randn(T, (hq + 2 * hkv) * D, gen=g)
+    qkv[:, (hq + hkv) * D:] = float("nan")
+    pos = torch.randint(0, max_pos, (T,), generator=g, dtype=torch.int32)
+    table = ref.rope_table(D, max_pos, 1e6)
+    qw, kw = _randn(D, gen=g), _randn(D, gen=g)
+    q, k = qk_norm_rope(qkv.to(cuda_device), pos.to(cuda_device), table.to(cuda_device),
+                        qw.to(cuda_device), kw.to(cuda_device), EPS, hq, hkv)
+    wq, wk, _ = ref.qk_norm_rope(qkv, pos, table, qw, kw, EPS, hq, hkv)
+    assert q.shape == (T, hq, D) and k.shape == (T, hkv, D) and k.is_contiguous()
+    torch.testing.assert_close(q.cpu().float(), wq.float(), **TOL)
+    torch.testing.assert_close(k.cpu().float(), wk.float(), **TOL)
+    # the same kernel with the append writes the same k bits into the pages
+    bs, nb = 64, -(-T // 64) + 1
+    raw, pool, (kc, vc) = _pool(nb, bs, hkv, D, cuda_device, g)
+    slots = torch.arange(T, dtype=torch.int32)
+    q2 = qk_norm_rope_append(qkv.to(cuda_device), pos.to(cuda_device), table.to(cuda_device),
+                             qw.to(cuda_device), kw.to(cuda_device), EPS, hq, hkv, kc, vc, slots.to(cuda_device))
+    torch.cuda.synchronize()
+    assert torch.equal(q2.cpu().view(torch.int16), q.cpu().view(torch.int16))
+    got_k = kc.reshape(nb * bs, hkv, D)[:T].cpu()
+    assert torch.equal(got_k.view(torch.int16), k.cpu().view(torch.int16))
+
+
 def test_qk_norm_rope_without_append_and_bad_position(cuda_device):
     D, hq, hkv, T = 128, 16, 8, 4
     g = torch.Generator().manual_seed(3)
