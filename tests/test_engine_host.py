@@ -375,3 +375,48 @@ def test_second_request_hits_prefix_through_scheduler():
     assert seq2.stats.prefix_cache_hit_tokens == 12
     drive(sched)
     assert sched.block_manager.prefix_cache_hit_tokens == 12
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_workloads_keep_the_scheduler_invariants(seed):
+    """Random prompts (some sharing prefixes), budgets, seat limits and small pools,
+    driven to completion with ignore_eos.  Every step respects the token budget and the
+    seats; a prefill step admits in queue order, and a partial chunk (of a prompt longer
+    than the budget) is always the step's only sequence; a decode step schedules
+    one token per sequence; every request ends with exactly max_tokens tokens, and all
+    pages return to the free list."""
+    import random
+
+    rng = random.Random(seed)
+    budget = rng.choice([8, 13, 32, 64])
+    cfg = make_config(max_num_seqs=rng.choice([1, 2, 5, 8]), max_num_batched_tokens=budget,
+                      num_kvcache_blocks=rng.choice([12, 24, 64]))
+    sched = Scheduler(cfg)
+    shared = [rng.randrange(1, 50) for _ in range(8)]
+    seqs = []
+    for _ in range(rng.randrange(1, 10)):
+        n = rng.randrange(1, 30)
+        toks = (shared[:rng.randrange(0, 9)] + [rng.randrange(1, 50) for _ in range(n)])[:29] or [7]
+        seqs.append(make_seq(toks, max_tokens=rng.randrange(1, 12), ignore_eos=True))
+    for s in seqs:
+        sched.add(s)
+    pool = cfg.num_kvcache_blocks
+    steps = 0
+    while not sched.is_finished():
+        waiting_before = list(sched.waiting)
+        batch, is_prefill = sched.schedule()
+        assert batch and len(batch) <= cfg.max_num_seqs
+        if is_prefill:
+            assert sum(s.num_scheduled_tokens for s in batch) <= budget
+            assert batch == waiting_before[:len(batch)]       # admitted in queue order
+            partial = [s for s in batch if s.num_cached_tokens + s.num_scheduled_tokens < s.num_tokens]
+            # only a step's sole sequence runs a partial chunk, and it fills the budget
+            assert not partial or (batch == partial and batch[0].num_scheduled_tokens == budget)
+        else:
+            assert all(s.num_scheduled_tokens == 1 for s in batch)
+            assert all(len(s.block_table) * BS >= s.num_tokens for s in batch)
+        sched.postprocess(batch, [5] * len(batch), is_prefill)
+        steps += 1
+        assert steps < 5000
+    assert all(s.is_finished and s.num_completion_tokens == s.max_tokens for s in seqs)
+    assert len(sched.block_manager.free_block_ids) == pool
