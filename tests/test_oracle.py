@@ -96,6 +96,44 @@ def _decode_case(seed, B, hq, hkv, d, bs, max_ctx, nb):
     return q, kc, vc, bt, torch.tensor(ctx, dtype=torch.int32), k_log, v_log
 
 
+@pytest.mark.parametrize("layout", ["contiguous", "interleaved"])
+def test_torch_append_equals_the_byte_level_append(layout):
+    """The timed CPU baseline of the append (a torch index-put) writes exactly the bytes
+    of the byte-level restatement: valid slots copied, -1 skipped, every other byte of
+    the caches (for the page-interleaved pool: of the whole pool) untouched."""
+    g = gen(77)
+    nb, bs, hkv, d, n = 9, 64, 4, 128, 200
+    if layout == "contiguous":
+        kc = randn_bf16((nb, bs, hkv, d), g)
+        vc = randn_bf16((nb, bs, hkv, d), g)
+        base = torch.stack([kc, vc])
+
+        def copies():
+            store = base.clone()
+            return store[0], store[1], store
+    else:
+        pool, kc, _ = interleaved_pool(nb, bs, hkv, d, g)
+
+        def copies():  # fresh views into a copy of the pool, with the engine's strides
+            store = pool.clone()
+            k2, v2 = ref.page_views(store, bs, hkv, d)
+            assert k2.stride() == kc.stride()
+            return k2, v2, store
+    qkv = randn_bf16((n, 3 * hkv * d), g)
+    key = randn_bf16((n, hkv, d), g)                                    # contiguous rows
+    value = qkv[:, 2 * hkv * d:].view(n, hkv, d)                         # strided rows
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(torch.int32)
+    slots[::5] = -1
+    want_k, want_v, want = copies()
+    ref.kv_append(ref.bf16_bits(key), ref.bf16_bits(value.contiguous()), ref.bf16_bits(want_k),
+                  ref.bf16_bits(want_v), slots.numpy())
+    got_k, got_v, got = copies()
+    ref.torch_append(key, value, got_k, got_v, slots)
+    assert torch.equal(got.view(torch.uint8), want.view(torch.uint8))
+    _, _, before = copies()
+    assert not torch.equal(got.view(torch.uint8), before.view(torch.uint8))  # it did write
+
+
 def test_decode_matches_sdpa_with_gqa():
     """Against torch SDPA(enable_gqa=True) on the logical (unpaged) K/V.  Catches: wrong
     gather through the block table, wrong GQA head map, scale applied twice or not at all."""
