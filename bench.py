@@ -892,7 +892,7 @@ def e2e_workload(num_seqs: int = 256, seed: int = 0):
     return prompts, max_tokens
 
 
-def bench_e2e(num_seqs: int = 256, caller: str = "fused"):
+def bench_e2e(num_seqs: int = 256, caller: str = "fused", fused_decode: bool = True):
     """Offline generation with the Qwen3-0.6B architecture (random bf16 weights), greedy,
     ignore_eos, hipGraph decode, max_model_len 4096: output tok/s = sum(max_tokens) / wall.
     caller "dropin" runs the layers in the reference's order (q/k norm + RoPE, then
@@ -901,7 +901,8 @@ def bench_e2e(num_seqs: int = 256, caller: str = "fused"):
     from kavor_amd.sampling_params import SamplingParams
 
     t0 = time.perf_counter()
-    llm = LLM(None, enforce_eager=False, max_model_len=4096, seed=0, attention_caller=caller)
+    llm = LLM(None, enforce_eager=False, max_model_len=4096, seed=0, attention_caller=caller,
+              fused_decode=fused_decode)
     init_s = time.perf_counter() - t0
     print(f"e2e: engine ready in {init_s:.1f}s ({llm.config.num_kvcache_blocks} pages, "
           f"{len(llm.model_runner.graphs)} graphs)", file=sys.stderr, flush=True)
@@ -928,7 +929,8 @@ def bench_e2e(num_seqs: int = 256, caller: str = "fused"):
         init_s=round(init_s, 2), capture_s=round(runner.timings["capture"], 2),
         workload=f"{num_seqs} requests, prompt U[100,1024] ids uniform over 151936, output U[100,1024], "
                  "greedy, ignore_eos, Qwen3-0.6B arch random bf16 weights, max_model_len 4096, "
-                 f"hipGraph decode, block 256, {caller} attention caller",
+                 f"hipGraph decode, block 256, {caller} attention caller"
+                 + (", one-launch decode step" if caller == "fused" and fused_decode else ""),
     )
     llm.exit()
     del llm
@@ -1126,6 +1128,9 @@ def main() -> int:
         del inp
         torch.cuda.empty_cache()
         extras["e2e_qwen3_0.6b"] = bench_e2e(args.e2e_seqs)
+        d = bench_e2e(args.e2e_seqs, fused_decode=False)
+        extras["e2e_qwen3_0.6b"]["separate_decode_launches"] = {
+            k: d[k] for k in ("output_tok_s", "decode_tok_s", "wall_s", "workload")}
         d = bench_e2e(args.e2e_seqs, caller="dropin")
         extras["e2e_qwen3_0.6b"]["dropin"] = {k: d[k] for k in ("output_tok_s", "decode_tok_s", "wall_s",
                                                                "prefill_tok_s", "workload")}

@@ -115,6 +115,40 @@ int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_t q_head_st
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Decode step of a Qwen3 attention layer in one launch: q/k RMSNorm + neox RoPE of the
+ * decode token, its K/V append, and paged decode attention.  Row b of qkv holds the token's
+ * num_q_heads q heads, then num_kv_heads k heads, then num_kv_heads v heads (the fused
+ * qkv projection output, kavor/models/qwen3.py:80-88).  For each sequence b the kernel
+ *   - normalises and rotates its q heads and k heads with q_norm_weight / k_norm_weight
+ *     and cos_sin at position context_lens[b] - 1, the decode token's position
+ *     (kvp_qk_norm_rope_append_bf16's arithmetic; a position outside the table gives a
+ *     NaN row);
+ *   - appends the rotated k and the raw v at slot_mapping[b] (skipped for -1 or a slot
+ *     outside the pool);
+ *   - attends over context_lens[b] tokens (kvp_paged_decode_bf16's arithmetic), of which
+ *     the last is this token: its k and v come from the qkv row, not from the cache, so
+ *     the launch never reads a slot it writes.
+ * slot_mapping[b] must be the slot of position context_lens[b] - 1 (as the engine builds
+ * decode metadata, model_runner.py:448-460) for the result to equal the separate calls.
+ * Rows without work (context 0, or longer than the block table) are not appended.  Replaces q_norm, k_norm, rotary_emb and Attention.forward's
+ * store_kvcache + flash_attn_with_kvcache in decode (qwen3.py:85-90;
+ * flash_attention_kvcache.py:71-83).  The workspace is kvp_paged_decode_bf16's.
+ */
+int kvp_paged_decode_fused_bf16(const void* qkv, int64_t qkv_tok_stride,
+                                const float* cos_sin, int32_t max_position,
+                                const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                void* k_cache, void* v_cache,
+                                int64_t cache_block_stride, int64_t cache_slot_stride,
+                                int64_t cache_head_stride, int32_t num_cache_blocks,
+                                const int32_t* slot_mapping,
+                                const int32_t* block_tables, int64_t block_table_stride,
+                                const int32_t* context_lens, int32_t num_seqs,
+                                int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t block_size, int32_t max_blocks_per_seq, float softmax_scale,
+                                void* out, int64_t out_seq_stride, int64_t out_head_stride,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * kvp_paged_decode_bf16 without a workspace argument: the decode's partial states live
  * in a static 32 MiB device array of the library (one per GPU, held until the process
  * ends), so the call allocates nothing and needs no caller buffer.  No counterpart in

@@ -49,6 +49,20 @@ SIGNATURES: dict[str, tuple] = {
         _c_void_p, _i64, _i64,            # out, out_seq_stride, out_head_stride
         _c_void_p, _size_t, _c_void_p,    # workspace, workspace_bytes, stream
     ]),
+    "kvp_paged_decode_fused_bf16": (ctypes.c_int, [
+        _c_void_p, _i64,                  # qkv, qkv_tok_stride
+        _c_void_p, _i32,                  # cos_sin, max_position
+        _c_void_p, _c_void_p, _f32,       # q_norm_weight, k_norm_weight, eps
+        _c_void_p, _c_void_p,             # k_cache, v_cache
+        _i64, _i64, _i64, _i32,           # cache block/slot/head strides, num_cache_blocks
+        _c_void_p,                        # slot_mapping
+        _c_void_p, _i64,                  # block_tables, block_table_stride
+        _c_void_p, _i32,                  # context_lens, num_seqs
+        _i32, _i32, _i32,                 # num_q_heads, num_kv_heads, head_dim
+        _i32, _i32, _f32,                 # block_size, max_blocks_per_seq, softmax_scale
+        _c_void_p, _i64, _i64,            # out, out_seq_stride, out_head_stride
+        _c_void_p, _size_t, _c_void_p,    # workspace, workspace_bytes, stream
+    ]),
     "kvp_paged_decode_bf16_noalloc": (ctypes.c_int, [
         _c_void_p, _i64, _i64,            # q, q_seq_stride, q_head_stride
         _c_void_p, _c_void_p,             # k_cache, v_cache

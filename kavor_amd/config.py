@@ -13,7 +13,9 @@ weights are random (seeded by `seed`).  Differences from the reference:
   normalises, rotates and appends k / v, then attention reads the pages) or "dropin"
   (the reference's order, kavor/models/qwen3.py:85-90: q/k norm + RoPE, then
   Attention.forward(q, k, v) appends through store_kvcache and runs dense varlen
-  prefill for batches without a cached prefix).
+  prefill for batches without a cached prefix);
+- fused_decode (with the fused caller) runs a decode step's q/k norm + RoPE, K/V append
+  and paged attention as one launch per layer instead of two.
 """
 
 from __future__ import annotations
@@ -39,6 +41,7 @@ class Config:
     num_kvcache_blocks: int = -1
     seed: int = 0
     attention_caller: str = "fused"
+    fused_decode: bool = True
     spec: Qwen3Spec = field(init=False)
     checkpoint: str | None = field(init=False, default=None)
 

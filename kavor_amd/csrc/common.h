@@ -74,6 +74,63 @@ __device__ __forceinline__ void store16_nt(void* ptr, uint4 v) {
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(ptr));
 }
 
+// Eight bf16 values of a 16-byte chunk, widened exactly to fp32, and back (RNE).
+__device__ __forceinline__ void unpack8(const uint4 w, float f[8]) {
+  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+__device__ __forceinline__ uint4 pack8(const float f[8]) {
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
+                    pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
+// x rounded to bf16 and back to fp32, as the eager path's intermediate bf16 tensors are
+// (round-to-nearest-even, the v_cvt_pk_bf16_f32 conversion).  A software rounding took
+// about 7 VALU operations per value, and RMSNorm and q/k norm round twice per element:
+// the fused q/k norm + RoPE + append at 16,384 tokens ran 51.4 -> 47.3 us with the
+// conversion, bit-identical.
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float(static_cast<u32>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(x))) << 16);
+}
+
+constexpr int kRopeDim = 128;  // head_dim of the q/k norm + RoPE code: 16 lanes x 8 elements
+
+// One head row held by a 16-lane DPP row, lane j owning elements 8j..8j+7: RMSNorm with
+// fp32 statistics, the bf16 rounding of the normalised value, the weight, a second bf16
+// rounding (the reference's two eager steps, kavor/layers/layernorm.py:235-258), then neox
+// RoPE in fp32 (rotary_embedding.py:8-53): element i < 64 pairs with i + 64, which lives
+// in lane j ^ 8 (DPP row_ror:8).  c / sn are this lane's cos / sin of frequencies
+// 8 (j & 7) .. +7; a position outside the table (pos_ok false) gives NaN.
+
+__device__ __forceinline__ void norm_rope_head(float (&x)[8], const float (&w)[8], const float (&c)[8],
+                                               const float (&sn)[8], bool first_half, bool pos_ok,
+                                               float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = row16_sum(ss);
+  const float rstd = rsqrtf(ss * (1.0f / kRopeDim) + eps);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = round_bf16(round_bf16(x[e] * rstd) * w[e]);
+  const uint4 mine = pack8(x);
+  uint4 other;
+  other.x = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.x), 0x128, 0xf, 0xf, false));
+  other.y = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.y), 0x128, 0xf, 0xf, false));
+  other.z = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.z), 0x128, 0xf, 0xf, false));
+  other.w = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mine.w), 0x128, 0xf, 0xf, false));
+  float y[8];
+  unpack8(other, y);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // first half: x1*cos - x2*sin; second half: x2*cos + x1*sin
+    const float o = first_half ? x[e] * c[e] - y[e] * sn[e] : x[e] * c[e] + y[e] * sn[e];
+    x[e] = pos_ok ? o : __builtin_nanf("");
+  }
+}
+
 // Lowest finite value used as the running-max floor of the online softmax, so that
 // exp2(m_old - m_new) never evaluates (-inf) - (-inf).
 constexpr float kMaxFloor = -1.0e30f;

@@ -44,6 +44,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 
@@ -82,6 +83,18 @@ struct DecodeParams {
   int32_t* header;  // [0] steps per range, [kHeaderInts ..] step prefix sums (B + 1)
   float* part_o;    // [slot][num_q_heads][128], slot = range + sequence (ranges + B slots)
   float* part_ml;   // [slot][num_q_heads][2] = (max, sum)
+  // Fused q/k norm + RoPE + append (FUSED kernels): row b of qkv holds the token's
+  // num_q_heads q heads, then num_kv_heads k heads, then num_kv_heads v heads.
+  // The token's position is context_lens[b] - 1.
+  const uint16_t* qkv;
+  int64_t qkv_stride;
+  const float* cos_sin;  // [max_position][128] fp32: cos of the 64 frequencies, then sin
+  int32_t max_position;
+  const uint16_t* q_weight;
+  const uint16_t* k_weight;
+  float eps;
+  const int32_t* slot_mapping;
+  int64_t num_cache_slots;
 };
 
 __device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
@@ -309,12 +322,183 @@ __device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh
   }
 }
 
-template <int G, int STEP>
+// ---- fused q/k norm + RoPE + append (FUSED kernels)
+//
+// The inputs of the q of a sequence (its cos/sin row and raw q heads) and of its new token
+// (cos/sin row, raw k and v heads) reach a per-wave LDS scratch with direct-to-LDS buffer
+// loads (buffer_load_dwordx4 ... lds: lane l writes 16 bytes at M0 + 16 l), issued one
+// step before they are needed, so the wave never waits on a dependent load chain at a
+// sequence boundary and no VGPR holds them meanwhile.  Each kind has two regions, one per
+// copy of the unrolled step loop; a region is read by the step copy that consumes it and
+// written only by the other copy.  A region read at the end of step S was filled during
+// step S - 1, after the K/V loads of step S and before those of step S + 1 (2 NL loads);
+// vector memory operations complete in issue order, so an explicit wait that leaves at
+// most 2 NL of them in flight covers it.  The compiler's own tracking of direct-to-LDS
+// loads does not order these reads, hence the explicit wait.  The global_load_lds form
+// is avoided: the compiler treats it as a flat access to both memories and waits for
+// every outstanding load at the next use of any loaded register.  Buffer loads are
+// range-checked against the resource's size by the hardware.  The token's position is
+// context_lens[b] - 1.
+constexpr int kFzRow = 512;  // bytes: one cos/sin row, 128 fp32
+constexpr int kFzNew = 1024;  // new token: cos/sin row | raw k head | raw v head
+template <int G>
+struct FzSize {  // q of a sequence: cos/sin row | G raw q heads, in 1 KiB loads
+  static constexpr int kLoads = (kFzRow + G * 256 + 1023) / 1024;
+  static constexpr int kBytes = kLoads * 1024;
+};
+
+typedef int32_t BufferRsrc __attribute__((ext_vector_type(4)));
+__device__ void raw_buffer_load_lds(BufferRsrc rsrc, __attribute__((address_space(3))) void* lds, int size,
+                                    int voffset, int soffset, int offset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+// Buffer resource over `bytes` bytes at `base` (stride 0, raw byte offsets).
+__device__ __forceinline__ BufferRsrc buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  BufferRsrc r;
+  r.x = static_cast<int32_t>(static_cast<uint32_t>(a));
+  r.y = static_cast<int32_t>((a >> 32) & 0xffffu);
+  r.z = static_cast<int32_t>(bytes);
+  r.w = 0x00020000;  // gfx9 word 3: 32-bit data format, no swizzle
+  return r;
+}
+
+// Waits until at most N vector memory operations of the wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// 16 bytes at byte offset voffset of the resource into LDS region + 16 * lane.
+__device__ __forceinline__ void lds_dma16(BufferRsrc rsrc, int voffset, char* region) {
+  raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)region, 16, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ BufferRsrc cos_sin_rsrc(const DecodeParams& p) {
+  return buffer_rsrc(p.cos_sin, static_cast<uint32_t>(p.max_position) * kFzRow);
+}
+__device__ __forceinline__ BufferRsrc qkv_rsrc(const DecodeParams& p) {
+  return buffer_rsrc(p.qkv, static_cast<uint32_t>(p.num_seqs * p.qkv_stride * 2));
+}
+__device__ __forceinline__ int fz_row_bytes(const DecodeParams& p, int ctx) {
+  const int pos = ctx - 1;
+  return (pos >= 0 && pos < p.max_position ? pos : 0) * kFzRow;
+}
+
+// Weights: lanes 0-15 the q norm weight, 16-31 the k norm weight.
+__device__ __forceinline__ void fz_issue_weights(const DecodeParams& p, int lane, char* region) {
+  if (lane < 16) lds_dma16(buffer_rsrc(p.q_weight, 256), 16 * lane, region);
+  else if (lane < 32) lds_dma16(buffer_rsrc(p.k_weight, 256), 16 * (lane - 16), region);
+}
+
+// q inputs of sequence b (context ctx) for kv head kvh: the cos/sin row at bytes 0-511,
+// then the G q heads.
+template <int G>
+__device__ __forceinline__ void fz_issue_q(const DecodeParams& p, int b, int ctx, int kvh, int lane, char* region) {
+  if (lane < 32) lds_dma16(cos_sin_rsrc(p), fz_row_bytes(p, ctx) + 16 * lane, region);
+  const int heads = (b * static_cast<int>(p.qkv_stride) + kvh * G * kRopeDim) * 2;
+#pragma unroll
+  for (int i = 0; i < FzSize<G>::kLoads; ++i) {
+    const int byte = 1024 * i + 16 * lane;  // this lane's destination within the region
+    if (byte >= kFzRow && byte < kFzRow + G * 256) lds_dma16(qkv_rsrc(p), heads + byte - kFzRow, region + 1024 * i);
+  }
+}
+
+// New-token inputs of sequence b (context ctx) for kv head kvh: the cos/sin row, then the
+// raw k head (bytes 512-767) and the raw v head (768-1023).
+__device__ __forceinline__ void fz_issue_new(const DecodeParams& p, int b, int ctx, int kvh, int lane, char* region) {
+  if (lane < 32) {
+    lds_dma16(cos_sin_rsrc(p), fz_row_bytes(p, ctx) + 16 * lane, region);
+  } else {
+    const int head = lane < 48 ? p.num_q_heads + kvh : p.num_q_heads + p.num_kv_heads + kvh;
+    lds_dma16(qkv_rsrc(p), (b * static_cast<int>(p.qkv_stride) + head * kRopeDim) * 2 + 16 * (lane & 15), region);
+  }
+}
+
+__device__ __forceinline__ void fz_cos_sin(const char* row, int c, float (&cs)[8], float (&sn)[8]) {
+  const float* f = reinterpret_cast<const float*>(row) + 8 * (c & 7);
+  *reinterpret_cast<float4*>(cs) = *reinterpret_cast<const float4*>(f);
+  *reinterpret_cast<float4*>(cs + 4) = *reinterpret_cast<const float4*>(f + 4);
+  *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(f + kRopeDim / 2);
+  *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(f + kRopeDim / 2 + 4);
+}
+
+// q of a sequence from its q region: RMS-normalised and rotated, in the decode's q layout
+// (lane c: dims 8c..8c+7 of every head).
+template <int G>
+__device__ __forceinline__ void fz_finish_q(const DecodeParams& p, int ctx, int c, const char* region,
+                                            const char* weights, uint4 (&qv)[G]) {
+  const bool pos_ok = ctx - 1 >= 0 && ctx - 1 < p.max_position;
+  float w[8], cs[8], sn[8];
+  unpack8(*reinterpret_cast<const uint4*>(weights + 16 * c), w);
+  fz_cos_sin(region, c, cs, sn);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float x[8];
+    unpack8(*reinterpret_cast<const uint4*>(region + kFzRow + 256 * g + 16 * c), x);
+    norm_rope_head(x, w, cs, sn, c < 8, pos_ok, p.eps);
+    qv[g] = pack8(x);
+  }
+}
+
+// The new token of sequence b: k normalised and rotated, v as is; both appended at
+// slot_mapping[b] (-1 or a slot outside the pool: not stored) by lanes 0-15, and folded
+// into the wave's online softmax as one more key (counted in lane row 0 only; the step
+// that loaded its slot masked it out).  Only the wave owning the sequence's final step of
+// kv head kvh runs this, so the appended token is never read from the cache in the launch.
+template <int G>
+__device__ __forceinline__ void fz_finish_new(const DecodeParams& p, int b, int ctx, int kvh, int r, int c,
+                                              const char* region, const char* weights, const uint4 (&qv)[G],
+                                              float (&m)[G], float (&l)[G], float (&acc)[G][8]) {
+  const bool pos_ok = ctx - 1 >= 0 && ctx - 1 < p.max_position;
+  const int slot = load_uniform(p.slot_mapping, b);
+  float w[8], cs[8], sn[8], x[8];
+  unpack8(*reinterpret_cast<const uint4*>(weights + 256 + 16 * c), w);
+  fz_cos_sin(region, c, cs, sn);
+  unpack8(*reinterpret_cast<const uint4*>(region + kFzRow + 16 * c), x);
+  const uint4 vraw = *reinterpret_cast<const uint4*>(region + kFzRow + 256 + 16 * c);
+  norm_rope_head(x, w, cs, sn, c < 8, pos_ok, p.eps);
+  const uint4 knew = pack8(x);
+  if (r == 0 && slot >= 0 && slot < p.num_cache_slots) {
+    const int blk = slot / p.block_size, off = slot - blk * p.block_size;
+    const int64_t at = static_cast<int64_t>(blk) * p.blk_stride + static_cast<int64_t>(off) * p.slot_stride +
+                       static_cast<int64_t>(kvh) * p.head_stride + 8 * c;
+    *reinterpret_cast<uint4*>(const_cast<uint16_t*>(p.k_cache) + at) = knew;
+    *reinterpret_cast<uint4*>(const_cast<uint16_t*>(p.v_cache) + at) = vraw;
+  }
+  const float vf[8] = {bf16_lo(vraw.x), bf16_hi(vraw.x), bf16_lo(vraw.y), bf16_hi(vraw.y),
+                       bf16_lo(vraw.z), bf16_hi(vraw.z), bf16_lo(vraw.w), bf16_hi(vraw.w)};
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float part = dot2_bf16(qv[g].x, knew.x, 0.f);
+    part = dot2_bf16(qv[g].y, knew.y, part);
+    part = dot2_bf16(qv[g].z, knew.z, part);
+    part = dot2_bf16(qv[g].w, knew.w, part);
+    const float sc = r == 0 ? row16_sum(part) * p.scale_log2 : -INFINITY;
+    const float m_new = fmaxf(m[g], sc);
+    const float alpha = fast_exp2(m[g] - m_new);
+    const float pr = fast_exp2(sc - m_new);
+    m[g] = m_new;
+    l[g] = l[g] * alpha + pr;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = acc[g][j] * alpha + pr * vf[j];
+  }
+}
+
+template <int G, int STEP, bool FUSED>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const DecodeParams p) {
   constexpr int NL = STEP / 4;  // dwordx4 loads per lane per tensor per step
   constexpr int kMinSteps = kMinRangeTokens / STEP;
   __shared__ int s_cum[kMaxSeqsPerLaunch + 1];
   __shared__ int s_part[kDecodeThreads];
+  // fused scratch, per wave: norm weights; q inputs and new-token inputs for each of the
+  // two copies of the step loop (distinct objects: see the fused helpers)
+  constexpr int kFzWaves = FUSED ? kDecodeWaves : 1;
+  __shared__ __attribute__((aligned(16))) char s_fw[kFzWaves][1024];
+  __shared__ __attribute__((aligned(16))) char s_fq0[kFzWaves][FUSED ? FzSize<G>::kBytes : 16];
+  __shared__ __attribute__((aligned(16))) char s_fq1[kFzWaves][FUSED ? FzSize<G>::kBytes : 16];
+  __shared__ __attribute__((aligned(16))) char s_fn0[kFzWaves][FUSED ? kFzNew : 16];
+  __shared__ __attribute__((aligned(16))) char s_fn1[kFzWaves][FUSED ? kFzNew : 16];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -351,10 +535,34 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   cursor_start_seq(p, cur, lo, __builtin_amdgcn_readfirstlane(S0 - s_cum[lo]));
   const int64_t head_off = static_cast<int64_t>(kvh) * p.head_stride + 8 * c;
 
+  const int fw = FUSED ? wave : 0;
+  // The next sequence after the one whose steps end at step S (S < S1 - 1): the first
+  // sequence with steps starting at S + 1.
+  auto seq_after = [&](int b, int S) {
+    int nb = b + 1;
+    while (s_cum[nb + 1] == S + 1) ++nb;
+    return __builtin_amdgcn_readfirstlane(nb);
+  };
   uint4 qv[G];
+  if (FUSED) {
+    // q of the first sequence (waited for here, once per wave), and, if step S0 ends it,
+    // its new token and the next sequence's q for copy 0 of the step loop
+    fz_issue_weights(p, lane, s_fw[fw]);
+    fz_issue_q<G>(p, cur.b, cur.ctx, kvh, lane, s_fq1[fw]);
+    if (cur.j + 1 == cur.nsteps) {
+      fz_issue_new(p, cur.b, cur.ctx, kvh, lane, s_fn0[fw]);
+      if (S0 + 1 < S1) {
+        const int nb = seq_after(cur.b, S0);
+        fz_issue_q<G>(p, nb, load_uniform(p.context_lens, nb), kvh, lane, s_fq0[fw]);
+      }
+    }
+    wait_vmem<0>();
+    fz_finish_q<G>(p, cur.ctx, c, s_fq1[fw], s_fw[fw], qv);
+  } else {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    qv[g] = load16(p.q + cur.b * p.q_seq_stride + (kvh * G + g) * p.q_head_stride + 8 * c);
+    for (int g = 0; g < G; ++g)
+      qv[g] = load16(p.q + cur.b * p.q_seq_stride + (kvh * G + g) * p.q_head_stride + 8 * c);
+  }
   float m[G], l[G], acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -370,29 +578,25 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 
   // One step: prefetch the next step into (kN, vN), compute (kC, vC), emit at the end
   // of a sequence or of the range.  Returns false when the range is done.
-  auto advance = [&](uint4 (&kC)[NL], uint4 (&vC)[NL], int nvC,
-                     uint4 (&kN)[NL], uint4 (&vN)[NL], int& nvN, int S) -> bool {
-    const bool more = S + 1 < S1;
-    const bool seq_end = cur.j + 1 == cur.nsteps;
-    StepCursor nxt = cur;
-    uint4 qn[G];
-    if (more) {
-      if (seq_end) {
-        // next non-empty sequence: the one whose steps start at S + 1
-        int nb = cur.b + 1;
-        while (s_cum[nb + 1] == S + 1) ++nb;
-        nb = __builtin_amdgcn_readfirstlane(nb);
-        cursor_start_seq(p, nxt, nb, 0);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          qn[g] = load16(p.q + nb * p.q_seq_stride + (kvh * G + g) * p.q_head_stride + 8 * c);
-      } else {
-        nxt.j = cur.j + 1;
-      }
-      step_load<NL>(p, step_base<STEP>(p, nxt, head_off, nvN), nvN, r, kN, vN);
+  // Compute of the step held in (kC, vC), the fused new token at a sequence end, the emit
+  // at the end of a sequence or of the range, and with MORE the switch to the next
+  // sequence's q.  The last step of a range gets its own instance: where the path that
+  // prefetched the next step met the one that did not, the compiler would keep the
+  // smaller wait count of the two and stall on the prefetch.
+  auto finish = [&](const uint4 (&kC)[NL], const uint4 (&vC)[NL], int nvC, bool seq_end, const StepCursor& nxt,
+                    const uint4 (&qn)[G], char* fq_mine, char* fn_mine, auto more_c) {
+    constexpr bool MORE = decltype(more_c)::value;
+    // Fused: the sequence's last token is not read from the cache (it is appended by this
+    // launch) but folded in from the qkv row after the step.
+    step_compute<G, NL>(p, qv, kC, vC, FUSED && seq_end ? nvC - 1 : nvC, r, m, l, acc);
+    if (FUSED && seq_end) {
+      // this sequence's new-token region and, with MORE, the next one's q region were
+      // filled before the K/V loads of the next step
+      if (MORE) wait_vmem<2 * NL>();
+      else wait_vmem<0>();
+      fz_finish_new<G>(p, cur.b, cur.ctx, kvh, r, c, fn_mine, s_fw[fw], qv, m, l, acc);
     }
-    step_compute<G, NL>(p, qv, kC, vC, nvC, r, m, l, acc);
-    if (seq_end || !more) {
+    if (!MORE || seq_end) {
       const int cb = s_cum[cur.b], cb1 = s_cum[cur.b + 1];
       const int np = num_parts(cb, cb1, spr);
       emit_state<G>(p, cur.b, kvh, range + cur.b, np == 1, cur.bad, lane, m, l, acc);
@@ -403,18 +607,63 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
       }
-      if (more) {
+      if (MORE) {
+        if (FUSED) {
+          fz_finish_q<G>(p, nxt.ctx, c, fq_mine, s_fw[fw], qv);
+        } else {
 #pragma unroll
-        for (int g = 0; g < G; ++g) qv[g] = qn[g];
+          for (int g = 0; g < G; ++g) qv[g] = qn[g];
+        }
       }
     }
-    cur = nxt;
-    return more;
+  };
+
+  // One step: prefetch the next step into (kN, vN), then finish this one.  Returns false
+  // when the range is done.
+  auto advance = [&](uint4 (&kC)[NL], uint4 (&vC)[NL], int nvC,
+                     uint4 (&kN)[NL], uint4 (&vN)[NL], int& nvN, int S, auto copy) -> bool {
+    constexpr int X = decltype(copy)::value;  // this copy of the step loop (0 or 1)
+    char* fq_mine = X == 0 ? s_fq0[fw] : s_fq1[fw];
+    char* fn_mine = X == 0 ? s_fn0[fw] : s_fn1[fw];
+    char* fq_other = X == 0 ? s_fq1[fw] : s_fq0[fw];
+    char* fn_other = X == 0 ? s_fn1[fw] : s_fn0[fw];
+    const bool seq_end = cur.j + 1 == cur.nsteps;
+    if (S + 1 < S1) {
+      StepCursor nxt = cur;
+      uint4 qn[G];
+      if (seq_end) {
+        // next non-empty sequence: the one whose steps start at S + 1
+        const int nb = seq_after(cur.b, S);
+        cursor_start_seq(p, nxt, nb, 0);
+        if (!FUSED) {
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+            qn[g] = load16(p.q + nb * p.q_seq_stride + (kvh * G + g) * p.q_head_stride + 8 * c);
+        }
+      } else {
+        nxt.j = cur.j + 1;
+      }
+      step_load<NL>(p, step_base<STEP>(p, nxt, head_off, nvN), nvN, r, kN, vN);
+      if (FUSED && nxt.j + 1 == nxt.nsteps) {
+        // step S + 1 (the other copy) ends sequence nxt.b: its new token, and the q of the
+        // sequence after it, for that copy
+        fz_issue_new(p, nxt.b, nxt.ctx, kvh, lane, fn_other);
+        if (S + 2 < S1) {
+          const int nb2 = seq_after(nxt.b, S + 1);
+          fz_issue_q<G>(p, nb2, load_uniform(p.context_lens, nb2), kvh, lane, fq_other);
+        }
+      }
+      finish(kC, vC, nvC, seq_end, nxt, qn, fq_mine, fn_mine, std::true_type{});
+      cur = nxt;
+      return true;
+    }
+    finish(kC, vC, nvC, seq_end, cur, qv, fq_mine, fn_mine, std::false_type{});
+    return false;
   };
 
   for (int S = S0;; S += 2) {
-    if (!advance(kA, vA, nvA, kB, vB, nvB, S)) break;
-    if (!advance(kB, vB, nvB, kA, vA, nvA, S + 1)) break;
+    if (!advance(kA, vA, nvA, kB, vB, nvB, S, std::integral_constant<int, 0>{})) break;
+    if (!advance(kB, vB, nvB, kA, vA, nvA, S + 1, std::integral_constant<int, 1>{})) break;
   }
 }
 
@@ -521,9 +770,9 @@ static int64_t decode_workspace_bound(int64_t seqs, int64_t q_heads, int64_t max
   return decode_workspace_need(seqs, q_heads, ranges);
 }
 
-// Workgroups of paged_decode_kernel<G> resident on the whole current device (cached per
-// device once the queries succeed), capped at kMaxDecodeGrid.
-template <int G, int STEP>
+// Workgroups of paged_decode_kernel<G, STEP, FUSED> resident on the whole current device
+// (cached per device once the queries succeed), capped at kMaxDecodeGrid.
+template <int G, int STEP, bool FUSED>
 static int resident_workgroups() {
   static std::atomic<int> cached[16];
   int dev = 0;
@@ -533,7 +782,7 @@ static int resident_workgroups() {
   int cus = 0, per_cu = 0;
   bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
   if (!ok) cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<G, STEP>, kDecodeThreads, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<G, STEP, FUSED>, kDecodeThreads, 0) !=
           hipSuccess || per_cu <= 0) {
     per_cu = 1;
     ok = false;
@@ -543,27 +792,28 @@ static int resident_workgroups() {
   return v;
 }
 
-template <int G, int STEP>
+template <int G, int STEP, bool FUSED>
 static int64_t decode_ranges(int num_kv_heads, int64_t max_tokens) {
   const int64_t groups_per_range = (num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
-  return std::max<int64_t>(1, std::min<int64_t>(resident_workgroups<G, STEP>() / groups_per_range,
+  return std::max<int64_t>(1, std::min<int64_t>(resident_workgroups<G, STEP, FUSED>() / groups_per_range,
                                                 range_cap(max_tokens)));
 }
 
+template <bool FUSED>
 static int64_t decode_ranges_for(int G, int num_kv_heads, int64_t max_tokens) {
   switch (G) {
-    case 1: return decode_ranges<1, 32>(num_kv_heads, max_tokens);
-    case 2: return decode_ranges<2, 32>(num_kv_heads, max_tokens);
-    case 4: return decode_ranges<4, 32>(num_kv_heads, max_tokens);
-    default: return decode_ranges<8, kMinStepTokens>(num_kv_heads, max_tokens);
+    case 1: return decode_ranges<1, 32, FUSED>(num_kv_heads, max_tokens);
+    case 2: return decode_ranges<2, 32, FUSED>(num_kv_heads, max_tokens);
+    case 4: return decode_ranges<4, 32, FUSED>(num_kv_heads, max_tokens);
+    default: return decode_ranges<8, kMinStepTokens, FUSED>(num_kv_heads, max_tokens);
   }
 }
 
-template <int G, int STEP>
+template <int G, int STEP, bool FUSED>
 static void launch_decode(DecodeParams p, int64_t ranges, hipStream_t s) {
   const int64_t groups_per_range = (p.num_kv_heads + kDecodeWaves - 1) / kDecodeWaves;
   p.step_tokens = STEP;
-  hipLaunchKernelGGL((paged_decode_kernel<G, STEP>), dim3(static_cast<unsigned>(ranges * groups_per_range)),
+  hipLaunchKernelGGL((paged_decode_kernel<G, STEP, FUSED>), dim3(static_cast<unsigned>(ranges * groups_per_range)),
                      dim3(kDecodeThreads), 0, s, p);
   hipLaunchKernelGGL(decode_merge_kernel, dim3((p.num_q_heads + kMergeHeads - 1) / kMergeHeads, p.num_seqs),
                      dim3(kMergeThreads), 0, s, p);
@@ -624,11 +874,17 @@ static int check_decode_args(const char* fn, const DecodeArgs& a) {
 // cover decode_workspace_need of every launch; checked by the callers).  Batches beyond
 // the LDS prefix table run as consecutive launches of up to 4096 sequences; they reuse
 // the workspace in stream order.
-static int enqueue_decode(const char* fn, const DecodeArgs& a, int64_t ranges, char* ws, hipStream_t s) {
+template <bool FUSED>
+static int enqueue_decode(const char* fn, const DecodeArgs& a, int64_t ranges, char* ws, hipStream_t s,
+                          const DecodeParams* fused = nullptr) {
   const int G = a.num_q_heads / a.num_kv_heads;
   for (int b0 = 0; b0 < a.num_seqs; b0 += kMaxSeqsPerLaunch) {
     const int nb = std::min(kMaxSeqsPerLaunch, a.num_seqs - b0);
-    DecodeParams p;
+    DecodeParams p = fused ? *fused : DecodeParams{};
+    if (FUSED) {  // this chunk's rows of the per-sequence inputs
+      p.qkv += b0 * p.qkv_stride;
+      p.slot_mapping += b0;
+    }
     p.q = static_cast<const uint16_t*>(a.q) + b0 * a.q_seq_stride;
     p.q_seq_stride = a.q_seq_stride;
     p.q_head_stride = a.q_head_stride;
@@ -654,10 +910,10 @@ static int enqueue_decode(const char* fn, const DecodeArgs& a, int64_t ranges, c
     p.part_o = reinterpret_cast<float*>(ws + kHeaderBytes);
     p.part_ml = p.part_o + static_cast<size_t>(ranges + nb) * a.num_q_heads * kDecodeHeadDim;
     switch (G) {
-      case 1: launch_decode<1, 32>(p, ranges, s); break;
-      case 2: launch_decode<2, 32>(p, ranges, s); break;
-      case 4: launch_decode<4, 32>(p, ranges, s); break;
-      default: launch_decode<8, kMinStepTokens>(p, ranges, s); break;
+      case 1: launch_decode<1, 32, FUSED>(p, ranges, s); break;
+      case 2: launch_decode<2, 32, FUSED>(p, ranges, s); break;
+      case 4: launch_decode<4, 32, FUSED>(p, ranges, s); break;
+      default: launch_decode<8, kMinStepTokens, FUSED>(p, ranges, s); break;
     }
     const int rc = launch_status(fn);
     if (rc != KVP_OK) return rc;
@@ -666,10 +922,11 @@ static int enqueue_decode(const char* fn, const DecodeArgs& a, int64_t ranges, c
 }
 
 // Launch ranges for the batch's first (largest) launch.
+template <bool FUSED = false>
 static int64_t batch_ranges(const DecodeArgs& a) {
   const int nb = std::min(a.num_seqs, kMaxSeqsPerLaunch);
   const int64_t max_tokens = static_cast<int64_t>(nb) * a.max_blocks_per_seq * a.block_size;
-  return decode_ranges_for(a.num_q_heads / a.num_kv_heads, a.num_kv_heads, max_tokens);
+  return decode_ranges_for<FUSED>(a.num_q_heads / a.num_kv_heads, a.num_kv_heads, max_tokens);
 }
 
 // ---------------------------------------------------------------- no-allocation variant
@@ -742,7 +999,8 @@ extern "C" int kvp_paged_decode_bf16(const void* q, int64_t q_seq_stride, int64_
     return fail(KVP_EWORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
     return fail(KVP_EINVAL, "%s: workspace must be 256-byte aligned", fn);
-  return enqueue_decode(fn, a, batch_ranges(a), static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+  return enqueue_decode<false>(fn, a, batch_ranges(a), static_cast<char*>(workspace),
+                               static_cast<hipStream_t>(stream));
 }
 
 extern "C" int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
@@ -776,5 +1034,61 @@ extern "C" int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride
   char* ws = nullptr;
   rc = scratch_address(fn, &ws);
   if (rc != KVP_OK) return rc;
-  return enqueue_decode(fn, a, ranges, ws, static_cast<hipStream_t>(stream));
+  return enqueue_decode<false>(fn, a, ranges, ws, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvp_paged_decode_fused_bf16(
+    const void* qkv, int64_t qkv_tok_stride, const float* cos_sin,
+    int32_t max_position, const void* q_norm_weight, const void* k_norm_weight, float eps,
+    void* k_cache, void* v_cache, int64_t cache_block_stride, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int32_t num_cache_blocks, const int32_t* slot_mapping,
+    const int32_t* block_tables, int64_t block_table_stride, const int32_t* context_lens,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t max_blocks_per_seq, float softmax_scale,
+    void* out, int64_t out_seq_stride, int64_t out_head_stride,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  static const char fn[] = "kvp_paged_decode_fused_bf16";
+  clear_error();
+  // q is read from the qkv rows: the q pointer and strides of the shared checks stand in
+  // for them (the q heads of row b start at qkv + b * qkv_tok_stride).
+  const DecodeArgs a = {qkv, qkv_tok_stride, kRopeDim, k_cache, v_cache, cache_block_stride,
+                        cache_slot_stride, cache_head_stride, num_cache_blocks, block_tables,
+                        block_table_stride, context_lens, num_seqs, num_q_heads, num_kv_heads,
+                        head_dim, block_size, max_blocks_per_seq, softmax_scale, out,
+                        out_seq_stride, out_head_stride};
+  int rc = check_decode_args(fn, a);
+  if (rc != KVP_OK) return rc;
+  if (!cos_sin || !q_norm_weight || !k_norm_weight || !slot_mapping)
+    return fail(KVP_EINVAL, "%s: null pointer", fn);
+  if (max_position < 1) return fail(KVP_EINVAL, "%s: max_position=%d", fn, max_position);
+  if (!aligned16(cos_sin) || !aligned16(q_norm_weight) || !aligned16(k_norm_weight) ||
+      (reinterpret_cast<uintptr_t>(slot_mapping) & 3u))
+    return fail(KVP_EINVAL, "%s: misaligned cos_sin / norm weights / slot_mapping", fn);
+  if (qkv_tok_stride < static_cast<int64_t>(num_q_heads + 2 * num_kv_heads) * head_dim)
+    return fail(KVP_EINVAL, "%s: qkv row stride %lld is shorter than (hq + 2 hkv) * head_dim", fn,
+                static_cast<long long>(qkv_tok_stride));
+  if (num_seqs == 0) return KVP_OK;
+  const int chunk_seqs = std::min(num_seqs, kMaxSeqsPerLaunch);
+  // the kernel addresses the table and one launch's qkv rows with 32-bit byte offsets
+  if (static_cast<int64_t>(max_position) * kRopeDim * 4 > INT32_MAX ||
+      static_cast<int64_t>(chunk_seqs) * qkv_tok_stride * 2 > INT32_MAX)
+    return fail(KVP_EINVAL, "%s: the cos/sin table or %d qkv rows exceed 2 GiB", fn, chunk_seqs);
+  const size_t need =
+      static_cast<size_t>(decode_workspace_bound(chunk_seqs, num_q_heads, max_blocks_per_seq, block_size));
+  if (!workspace || workspace_bytes < need)
+    return fail(KVP_EWORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(KVP_EINVAL, "%s: workspace must be 256-byte aligned", fn);
+  DecodeParams f{};
+  f.qkv = static_cast<const uint16_t*>(qkv);
+  f.qkv_stride = qkv_tok_stride;
+  f.cos_sin = cos_sin;
+  f.max_position = max_position;
+  f.q_weight = static_cast<const uint16_t*>(q_norm_weight);
+  f.k_weight = static_cast<const uint16_t*>(k_norm_weight);
+  f.eps = eps;
+  f.slot_mapping = slot_mapping;
+  f.num_cache_slots = static_cast<int64_t>(num_cache_blocks) * block_size;
+  return enqueue_decode<true>(fn, a, batch_ranges<true>(a), static_cast<char*>(workspace),
+                              static_cast<hipStream_t>(stream), &f);
 }

@@ -68,7 +68,8 @@ class ModelRunner:
         self.timings = {"load": 0.0, "pool": 0.0, "capture": 0.0}
 
         t0 = perf_counter()
-        self.model = Qwen3ForCausalLM(self.spec, self.device, caller=config.attention_caller)
+        self.model = Qwen3ForCausalLM(self.spec, self.device, caller=config.attention_caller,
+                                      fused_decode=config.fused_decode)
         if config.checkpoint is not None:
             tensors = load_checkpoint_tensors(config.checkpoint)
             self.model.load_hf_state({k: v.to(self.device) for k, v in tensors.items()})

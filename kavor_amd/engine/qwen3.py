@@ -6,6 +6,9 @@ The model is the caller of the path (kavor/models/qwen3.py:75-91).  Per layer:
   -> paged attention over the page pool (HIP) -> o GEMM -> add-RMSNorm (HIP)
   -> gate_up GEMM -> SiLU * up (HIP) -> down GEMM
 
+In decode the q/k norm + RoPE + append and the paged attention are one launch
+(kvp_paged_decode_fused_bf16) unless fused_decode is off.
+
 With caller="dropin" the attention block keeps the reference's order instead: q/k
 RMSNorm + RoPE (HIP, k into a fresh tensor), then Attention.forward(q, k, v) with v a
 view of the qkv rows, which appends k / v (store_kvcache) and runs varlen prefill
@@ -34,7 +37,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from kavor_amd.layers import fused
-from kavor_amd.layers.attention import Attention
+from kavor_amd.layers.attention import Attention, paged_decode_fused
 from kavor_amd.utils.context import get_context
 
 
@@ -117,9 +120,11 @@ def _weight(*shape, device, dtype) -> nn.Parameter:
 
 class Qwen3Attention(nn.Module):
 
-    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype, caller: str = "fused"):
+    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype, caller: str = "fused",
+                 fused_decode: bool = True):
         super().__init__()
         self.caller = caller
+        self.fused_decode = fused_decode and caller == "fused"
         self.num_heads = spec.num_attention_heads
         self.num_kv_heads = spec.num_key_value_heads
         self.head_dim = spec.head_dim
@@ -139,6 +144,14 @@ class Qwen3Attention(nn.Module):
         attn = self.attn
         k_cache, v_cache = attn.k_cache[0], attn.v_cache[0]
         bound = k_cache.numel() > 0 and v_cache.numel() > 0
+        context = get_context()
+        if self.fused_decode and bound and not context.is_prefill:
+            # q/k norm + RoPE + append + paged decode in one launch
+            o = paged_decode_fused(qkv, self.rope, self.q_norm.weight, self.k_norm.weight,
+                                   self.q_norm.eps, self.num_heads, self.num_kv_heads, k_cache, v_cache,
+                                   context.slot_mapping, context.context_lens, context.block_tables,
+                                   attn.scale)
+            return F.linear(o.reshape(qkv.shape[0], self.q_size), self.o_proj)
         q = fused.qk_norm_rope_append(
             qkv, positions, self.rope, self.q_norm.weight, self.k_norm.weight, self.q_norm.eps,
             self.num_heads, self.num_kv_heads, k_cache if bound else None, v_cache if bound else None,
@@ -172,9 +185,10 @@ class Qwen3MLP(nn.Module):
 
 class Qwen3DecoderLayer(nn.Module):
 
-    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype, caller: str = "fused"):
+    def __init__(self, spec: Qwen3Spec, rope: torch.Tensor, device, dtype, caller: str = "fused",
+                 fused_decode: bool = True):
         super().__init__()
-        self.self_attn = Qwen3Attention(spec, rope, device, dtype, caller)
+        self.self_attn = Qwen3Attention(spec, rope, device, dtype, caller, fused_decode)
         self.mlp = Qwen3MLP(spec, device, dtype)
         self.input_layernorm = RMSNorm(spec.hidden_size, spec.rms_norm_eps, device, dtype)
         self.post_attention_layernorm = RMSNorm(spec.hidden_size, spec.rms_norm_eps, device, dtype)
@@ -192,7 +206,8 @@ class Qwen3DecoderLayer(nn.Module):
 class Qwen3ForCausalLM(nn.Module):
     """Qwen3 causal LM over the paged KV cache (bf16 weights on one GPU)."""
 
-    def __init__(self, spec: Qwen3Spec, device, dtype=torch.bfloat16, caller: str = "fused"):
+    def __init__(self, spec: Qwen3Spec, device, dtype=torch.bfloat16, caller: str = "fused",
+                 fused_decode: bool = True):
         super().__init__()
         self.spec = spec
         # prefill attention reads the pages (block tables on every prefill) when the layers
@@ -203,7 +218,8 @@ class Qwen3ForCausalLM(nn.Module):
         self.register_buffer("rope_table", rope, persistent=False)
         self.embed_tokens = _weight(spec.vocab_size, spec.hidden_size, device=device, dtype=dtype)
         self.layers = nn.ModuleList(
-            [Qwen3DecoderLayer(spec, rope, device, dtype, caller) for _ in range(spec.num_hidden_layers)])
+            [Qwen3DecoderLayer(spec, rope, device, dtype, caller, fused_decode)
+             for _ in range(spec.num_hidden_layers)])
         self.norm = RMSNorm(spec.hidden_size, spec.rms_norm_eps, device, dtype)
         self.lm_head = (self.embed_tokens if spec.tie_word_embeddings
                         else _weight(spec.vocab_size, spec.hidden_size, device=device, dtype=dtype))

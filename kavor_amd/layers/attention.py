@@ -21,7 +21,7 @@ from kavor_amd._lib import check, lib
 from kavor_amd.utils.context import get_context
 
 __all__ = [
-    "store_kvcache", "paged_decode", "varlen_prefill", "Attention",
+    "store_kvcache", "paged_decode", "paged_decode_fused", "varlen_prefill", "Attention",
     "reserve_decode_workspace", "decode_workspace_bytes",
     "flash_attn_with_kvcache", "flash_attn_varlen_func",
 ]
@@ -174,6 +174,53 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         out3.data_ptr(), out3.stride(0), out3.stride(1),
         ws.data_ptr(), ws.numel(), _stream(q3))
     check("kvp_paged_decode_bf16", rc)
+    return out
+
+
+def paged_decode_fused(qkv: torch.Tensor, cos_sin: torch.Tensor,
+                       q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
+                       num_q_heads: int, num_kv_heads: int, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, slot_mapping: torch.Tensor, cache_seqlens: torch.Tensor,
+                       block_table: torch.Tensor, softmax_scale: float,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """A Qwen3 decode step of one attention layer in one launch: q/k RMSNorm + RoPE of
+    each sequence's new token from its qkv row, the append of its k / v at slot_mapping,
+    and paged decode attention over cache_seqlens tokens (the last one being the new
+    token).  Returns [B, Hq, 128] bf16.  The token's position is cache_seqlens - 1 and
+    slot_mapping must hold the slot of that position, as the engine's decode metadata
+    has them."""
+    B = qkv.shape[0]
+    D = k_cache.shape[-1]
+    for name, t in (("qkv", qkv), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_cuda_bf16(name, t)
+    if qkv.dim() != 2 or qkv.stride(1) != 1 or qkv.shape[1] != (num_q_heads + 2 * num_kv_heads) * D:
+        raise ValueError("qkv must be [B, (Hq + 2 Hkv) * head_dim] with contiguous rows")
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share shape and strides")
+    num_blocks, block_size, Hkv, _ = k_cache.shape
+    if Hkv != num_kv_heads:
+        raise ValueError("cache heads do not match num_kv_heads")
+    for name, t in (("slot_mapping", slot_mapping), ("cache_seqlens", cache_seqlens)):
+        _require_int32(name, t, qkv.device)
+        if t.numel() < B:
+            raise ValueError(f"{name} has fewer rows than qkv")
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.shape[1] != D:
+        raise ValueError("cos_sin must be a contiguous fp32 [max_position, head_dim] table")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be an int32 [B, max_blocks] tensor with contiguous rows")
+    if out is None:
+        out = torch.empty(B, num_q_heads, D, dtype=torch.bfloat16, device=qkv.device)
+    max_blocks = block_table.shape[1]
+    ws = reserve_decode_workspace(B, num_q_heads, D, max_blocks, block_size, qkv.device)
+    rc = lib().kvp_paged_decode_fused_bf16(
+        qkv.data_ptr(), qkv.stride(0), cos_sin.data_ptr(), cos_sin.shape[0],
+        q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(eps),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        num_blocks, slot_mapping.data_ptr(), block_table.data_ptr(), block_table.stride(0),
+        cache_seqlens.data_ptr(), B, num_q_heads, num_kv_heads, D, block_size, max_blocks,
+        float(softmax_scale), out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), ws.numel(), _stream(qkv))
+    check("kvp_paged_decode_fused_bf16", rc)
     return out
 
 

@@ -200,3 +200,19 @@ def test_dropin_caller_order_matches_reference(cuda_device, monkeypatch):
     finally:
         llm.exit()
 
+
+def test_separate_decode_launches_match_reference(cuda_device):
+    """fused_decode off: the decode step runs the q/k norm + RoPE + append kernel and the
+    paged decode as two launches (the layout of the previous engine); graphs, padding and
+    prefix hits as in the default engine."""
+    llm = LLM(TINY, kvcache_block_size=64, max_model_len=1024, num_kvcache_blocks=128,
+              max_num_seqs=8, max_num_batched_tokens=1024, fused_decode=False, seed=0)
+    try:
+        assert not llm.model_runner.model.layers[0].self_attn.fused_decode
+        prompts = _prompts(15, [3, 70, 129, 256, 40])
+        sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True) for m in (20, 9, 33, 12, 5)]
+        outs = llm.generate(prompts, sps)
+        _check(llm, prompts, outs)
+    finally:
+        llm.exit()
+
