@@ -57,6 +57,17 @@ def decode_bytes(context_lens, num_q_heads: int, num_kv_heads: int, head_dim: in
     return 2 * kv_row * sum(ctx) + 2 * len(ctx) * num_q_heads * head_dim * 2 + 4 * (len(ctx) + blocks)
 
 
+def fused_decode_bytes(context_lens, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                       block_size: int) -> int:
+    """Algorithmic HBM bytes of one one-launch decode step: the paged decode's bytes with
+    the qkv row read in place of q, the new token's K and V written instead of read, one
+    fp32 cos/sin row (4 x head_dim B) and the int32 slot per sequence."""
+    B = len(context_lens)
+    qkv_extra = B * 2 * num_kv_heads * head_dim * 2  # the qkv row is q plus k and v
+    return (decode_bytes(context_lens, num_q_heads, num_kv_heads, head_dim, block_size) + qkv_extra
+            + B * (4 * head_dim + 4))
+
+
 def append_bytes(slot_mapping, num_kv_heads: int, head_dim: int) -> int:
     """Algorithmic HBM bytes of one KV append: K and V of each valid (non-negative) slot
     read once and written once (bf16), plus the int32 slot_mapping."""
@@ -165,6 +176,49 @@ def bench_decode(dev, steps, warmup, shape):
     ms = time_launches(step, steps, warmup)
     nbytes = decode_bytes(inp["ctx_host"].tolist(), inp["hq"], inp["hkv"], D, BS)
     return inp, dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+
+
+def bench_decode_step(dev, steps, warmup):
+    """One Qwen3-0.6B attention layer's decode work at the headline shape (256 sequences,
+    16q/8kv heads, contexts U[100, 2048]): the q/k norm + RoPE + append kernel followed by
+    paged decode, against the one-launch decode step over the same qkv rows, pools and
+    slots.  Graph-replayed, 10 calls per graph."""
+    from kavor_amd.engine.qwen3 import rope_cache
+    from kavor_amd.layers.attention import paged_decode, paged_decode_fused
+    from kavor_amd.layers.fused import qk_norm_rope_append
+
+    inp = decode_inputs(dev, 256, 16, 8, 100, 2048, 4096)
+    hq, hkv, B = inp["hq"], inp["hkv"], inp["q"].shape[0]
+    ctx, bt = inp["ctx_host"].tolist(), inp["bt_host"]
+    slots = torch.tensor([int(bt[b, (c - 1) // BS]) * BS + (c - 1) % BS for b, c in enumerate(ctx)],
+                         dtype=torch.int32).to(dev)
+    pos = inp["ctx"] - 1
+    dg = torch.Generator(device=dev).manual_seed(1)
+    qkv = torch.randn(B, (hq + 2 * hkv) * D, generator=dg, device=dev).to(torch.bfloat16)
+    qw = (torch.rand(D, generator=dg, device=dev) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=dg, device=dev) + 0.5).to(torch.bfloat16)
+    table = rope_cache(D, 40960, 1e6, dev)
+    q = torch.empty(B, hq, D, dtype=torch.bfloat16, device=dev)
+    out = torch.empty_like(q)
+
+    def separate():
+        qk_norm_rope_append(qkv, pos, table, qw, kw, 1e-6, hq, hkv, inp["kc"], inp["vc"], slots, q_out=q)
+        paged_decode(q, inp["kc"], inp["vc"], inp["ctx"], inp["bt"], SCALE, out=out)
+
+    def fused():
+        paged_decode_fused(qkv, table, qw, kw, 1e-6, hq, hkv, inp["kc"], inp["vc"], slots, inp["ctx"],
+                           inp["bt"], SCALE, out=out)
+
+    res = {}
+    for name, fn in (("separate", separate), ("fused", fused)):
+        warm_for(fn, 0.5)
+        res[name] = time_graph(fn, steps, warmup, per_graph=10) * 1e3
+    nbytes = fused_decode_bytes(ctx, hq, hkv, D, BS)
+    del inp
+    return dict(separate_us=round(res["separate"], 2), fused_us=round(res["fused"], 2), bytes=nbytes,
+                gbs=round(nbytes / res["fused"] / 1e3, 1), frac=round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4),
+                workload="one Qwen3-0.6B layer's decode: B=256, 16q/8kv, ctx U[100,2048], qkv rows -> "
+                         "q/k norm + RoPE + append + paged decode, graph-replayed")
 
 
 def bench_append(dev, steps, warmup):
@@ -583,6 +637,8 @@ def run_extras(dev, steps: int, warmup: int, cpu_baseline: bool = False) -> dict
     torch.cuda.empty_cache()
     extras["layer_kernels"] = bench_layers(dev, *n["layers"])
     torch.cuda.empty_cache()
+    extras["decode_step_fused"] = bench_decode_step(dev, *n["layers"])
+    torch.cuda.empty_cache()
     inp8, c = bench_decode(dev, *n["decode_8b"], "qwen3_8b")
     extras["paged_decode_qwen3_8b"] = dict(gbs=round(c["gbs"], 1), frac=round(c["gbs"] / HBM_PEAK_GBS, 4),
                                            ms=round(c["ms"], 4), bytes=c["bytes"],
@@ -722,14 +778,15 @@ def summarize_prefill_pmc(dir_a: str, dir_b: str) -> int:
 
 # (profile file, kernel-name prefix, which occurrence group, algorithmic bytes or flops, unit)
 PROFILE_KERNELS = [
-    ("paged_decode_qwen3_0.6b", "void kvp::paged_decode_kernel<2,", "decode_0.6b"),
-    ("paged_decode_qwen3_8b", "void kvp::paged_decode_kernel<4,", "decode_8b"),
+    ("paged_decode_qwen3_0.6b", "void kvp::paged_decode_kernel<2, 32, false>", "decode_0.6b"),
+    ("paged_decode_fused_qwen3_0.6b", "void kvp::paged_decode_kernel<2, 32, true>", "decode_fused_0.6b"),
+    ("paged_decode_qwen3_8b", "void kvp::paged_decode_kernel<4, 32, false>", "decode_8b"),
     ("kv_append_4096tok", "void kvp::kv_append_kernel<128", "append"),
     ("varlen_prefill_prefix_32seq", "void kvp::varlen_prefill_kernel<2, true, true>", "prefill"),
     ("qk_norm_rope_append_16384tok", "void kvp::(anonymous namespace)::qk_norm_rope_append_kernel<4>", "qk_norm_rope_append"),
     ("add_rmsnorm_16384x1024", "void kvp::(anonymous namespace)::rmsnorm_kernel<64, 2>", "add_rmsnorm"),
     ("silu_mul_16384x3072", "kvp::(anonymous namespace)::silu_mul_kernel", "silu_mul"),
-    ("argmax_256x151936", "kvp::(anonymous namespace)::argmax_kernel", "argmax"),
+    ("argmax_256x151936", "void kvp::(anonymous namespace)::argmax_kernel<1024, 3, false>", "argmax"),
 ]
 
 
@@ -762,6 +819,7 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
     f_scale, w_scale = gib_kib / copy_f, gib_kib / copy_w
     algo = {  # algorithmic bytes (flops for prefill) per launch of each workload
         "decode_0.6b": _decode_algo_bytes(256, 16, 100, 2048, 4096),
+        "decode_fused_0.6b": _decode_algo_bytes(256, 16, 100, 2048, 4096, fused=True),
         "decode_8b": _decode_algo_bytes(128, 32, 1024, 32768, 20000),
         "append": 32522240,
         "prefill": 352688504832,
@@ -861,10 +919,10 @@ def summarize_e2e(trace_dir: str, caller: str = "fused") -> int:
     return 0
 
 
-def _decode_algo_bytes(B, hq, lo, hi, pool_blocks, seed=0):
+def _decode_algo_bytes(B, hq, lo, hi, pool_blocks, seed=0, fused=False):
     g = torch.Generator().manual_seed(seed)
     ctx = torch.randint(lo, hi + 1, (B,), generator=g, dtype=torch.int32)
-    return decode_bytes(ctx.tolist(), hq, 8, D, BS)
+    return (fused_decode_bytes if fused else decode_bytes)(ctx.tolist(), hq, 8, D, BS)
 
 
 # ----------------------------------------------------------------------------- end to end

@@ -295,6 +295,22 @@ def decode_bytes(context_lens, num_q_heads: int, num_kv_heads: int, head_dim: in
     return kv + qo + meta
 
 
+def fused_decode_bytes(context_lens, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                       block_size: int, elem: int = 2) -> int:
+    """Algorithmic HBM bytes of one one-launch decode step (q/k norm + RoPE + append +
+    paged decode), counted sequence by sequence (contexts of at least one token): its qkv
+    row, fp32 cos/sin row, slot and context length read; its block-table entries read; the
+    K and V of its cached tokens (all but the new one) read; the new token's K and V and
+    its output written."""
+    total = 0
+    for c in (int(x) for x in context_lens):
+        total += (num_q_heads + 2 * num_kv_heads) * head_dim * elem + head_dim * 4 + 4 + 4
+        total += math.ceil(c / block_size) * 4
+        total += (c - 1) * num_kv_heads * head_dim * elem * 2
+        total += num_kv_heads * head_dim * elem * 2 + num_q_heads * head_dim * elem
+    return total
+
+
 def append_bytes(slot_mapping, num_kv_heads: int, head_dim: int, elem: int = 2) -> int:
     """Algorithmic HBM bytes of one KV append: read + write of K and V for each valid
     token, plus the slot_mapping read."""

@@ -16,6 +16,15 @@ def test_decode_bytes_match_oracle():
         assert bench.decode_bytes(ctx, hq, hkv, 128, bs) == ref.decode_bytes(ctx, hq, hkv, 128, bs)
 
 
+def test_fused_decode_bytes_match_oracle():
+    rng = random.Random(3)
+    for _ in range(50):
+        ctx = [rng.choice([1, 2, 255, 256, 257, rng.randint(1, 40000)]) for _ in range(rng.randint(1, 40))]
+        hq, hkv = rng.choice([(16, 8), (32, 8), (8, 1), (64, 8)])
+        bs = rng.choice([64, 256, 512])
+        assert bench.fused_decode_bytes(ctx, hq, hkv, 128, bs) == ref.fused_decode_bytes(ctx, hq, hkv, 128, bs)
+
+
 def test_append_bytes_match_oracle():
     rng = random.Random(1)
     for _ in range(50):
