@@ -572,9 +572,19 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
   }
 
+  // Tokens a step's loads may touch: with FUSED, a sequence's final step holds the token
+  // this launch appends, whose slot is not written yet; its rows are clamped onto the
+  // last cached token instead (a step with only the new token loads that slot but is
+  // never computed).
+  auto fused_load_count = [](const StepCursor& s, int nv) { return s.j + 1 == s.nsteps && nv > 1 ? nv - 1 : nv; };
   uint4 kA[NL], vA[NL], kB[NL], vB[NL];
   int nvA, nvB = 0;
-  step_load<NL>(p, step_base<STEP>(p, cur, head_off, nvA), nvA, r, kA, vA);
+  if constexpr (FUSED) {
+    const int64_t base = step_base<STEP>(p, cur, head_off, nvA);
+    step_load<NL>(p, base, fused_load_count(cur, nvA), r, kA, vA);
+  } else {
+    step_load<NL>(p, step_base<STEP>(p, cur, head_off, nvA), nvA, r, kA, vA);
+  }
 
   // One step: prefetch the next step into (kN, vN), compute (kC, vC), emit at the end
   // of a sequence or of the range.  Returns false when the range is done.
@@ -587,8 +597,14 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
                     const uint4 (&qn)[G], char* fq_mine, char* fn_mine, auto more_c) {
     constexpr bool MORE = decltype(more_c)::value;
     // Fused: the sequence's last token is not read from the cache (it is appended by this
-    // launch) but folded in from the qkv row after the step.
-    step_compute<G, NL>(p, qv, kC, vC, FUSED && seq_end ? nvC - 1 : nvC, r, m, l, acc);
+    // launch) but folded in from the qkv row after the step.  The step's loads were
+    // clamped onto the last cached token (fused_load_count), so no row holds the
+    // unwritten slot; a final step with no cached token is not computed at all.
+    if constexpr (FUSED) {
+      if (!(seq_end && nvC == 1)) step_compute<G, NL>(p, qv, kC, vC, seq_end ? nvC - 1 : nvC, r, m, l, acc);
+    } else {
+      step_compute<G, NL>(p, qv, kC, vC, nvC, r, m, l, acc);
+    }
     if (FUSED && seq_end) {
       // this sequence's new-token region and, with MORE, the next one's q region were
       // filled before the K/V loads of the next step
@@ -643,7 +659,12 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
       } else {
         nxt.j = cur.j + 1;
       }
-      step_load<NL>(p, step_base<STEP>(p, nxt, head_off, nvN), nvN, r, kN, vN);
+      if constexpr (FUSED) {
+        const int64_t base = step_base<STEP>(p, nxt, head_off, nvN);
+        step_load<NL>(p, base, fused_load_count(nxt, nvN), r, kN, vN);
+      } else {
+        step_load<NL>(p, step_base<STEP>(p, nxt, head_off, nvN), nvN, r, kN, vN);
+      }
       if (FUSED && nxt.j + 1 == nxt.nsteps) {
         // step S + 1 (the other copy) ends sequence nxt.b: its new token, and the q of the
         // sequence after it, for that copy

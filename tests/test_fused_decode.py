@@ -8,7 +8,8 @@ nothing else touched), and the attention output must match the fp32 oracle over 
 appended caches within atol 2e-2 / rtol 1e-2.  The new token is the last of its context
 and is folded in from registers rather than read back, so the cases cover contexts of
 one token, a new token that opens a page, contexts split across several work ranges,
-padding rows (context 0, slot -1) and a position outside the RoPE table.
+padding rows (context 0, slot -1) and a position outside the RoPE table; the slots being
+appended hold NaN before the call, as recycled page memory may.
 """
 
 import math
@@ -63,6 +64,13 @@ def test_fused_decode_equals_separate_launches(cuda_device, G, hkv, bs):
     ctxs = [1, 2, bs, bs + 1, 3 * bs - 1, 1500, 4000, 777]
     host, d1 = _case(cuda_device, 100 + G, hq, hkv, bs, ctxs, pad=3)
     d2 = {k: v.clone() for k, v in d1.items()}
+    # the slots the step appends hold NaN beforehand: nothing may read them before the
+    # append (a masked row times a NaN would still be NaN)
+    kc2, vc2 = ref.page_views(d2["pool"], bs, hkv, D)
+    for slot in host["slots"].tolist():
+        if slot >= 0:
+            kc2[slot // bs, slot % bs] = float("nan")
+            vc2[slot // bs, slot % bs] = float("nan")
     o_sep = _separate(d1, hq, hkv, bs)
     o_fused = _fused(d2, hq, hkv, bs)
     torch.cuda.synchronize()
