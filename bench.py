@@ -329,6 +329,9 @@ def layer_algo_bytes(inp) -> dict:
         "argmax": 256 * 151936 * 2 + 256 * 8,
         # a small decode batch: rows split over several workgroups
         "argmax_16rows": 16 * 151936 * 2 + 16 * 8,
+        # Gumbel-max sampling at T = 1 (bound by the Philox noise arithmetic, not HBM):
+        # logits and temperatures read, one int64 per row written
+        "sample_t1": 256 * 151936 * 2 + 256 * 4 + 256 * 8,
     }
 
 
@@ -339,6 +342,8 @@ def layer_launchers(inp):
     out = torch.empty_like(inp["x"])
     s_out = torch.empty(inp["T"], inp["I"], device=inp["x"].device, dtype=torch.bfloat16)
     tok = torch.empty(256, dtype=torch.int64, device=inp["x"].device)
+    temps = torch.ones(256, dtype=torch.float32, device=inp["x"].device)
+    seed = torch.zeros(1, dtype=torch.int32, device=inp["x"].device)
     return {
         "qk_norm_rope_append": lambda: fused.qk_norm_rope_append(
             inp["qkv"], inp["pos"], inp["table"], inp["qw"], inp["qw"], 1e-6, inp["hq"], inp["hkv"],
@@ -347,6 +352,7 @@ def layer_launchers(inp):
         "silu_mul": lambda: fused.silu_and_mul(inp["gu"], out=s_out),
         "argmax": lambda: fused.greedy_argmax(inp["logits"], out=tok),
         "argmax_16rows": lambda: fused.greedy_argmax(inp["logits"][:16], out=tok[:16]),
+        "sample_t1": lambda: fused.sample(inp["logits"], temps, seed, out=tok),
     }
 
 
@@ -362,7 +368,9 @@ def bench_layers(dev, steps, warmup):
         res[name] = dict(us=round(ms * 1e3, 2), gbs=round(algo[name] / ms / 1e6, 1),
                          frac=round(algo[name] / ms / 1e6 / HBM_PEAK_GBS, 4), bytes=algo[name])
     res["workload"] = (f"{inp['T']} tokens, Qwen3-0.6B layer (16q/8kv heads, hidden 1024, intermediate "
-                       "3072); argmax over [256, 151936] and [16, 151936] bf16 logits")
+                       "3072); argmax over [256, 151936] and [16, 151936] bf16 logits; sample_t1: "
+                       "Gumbel-max sampling of the [256, 151936] block at T = 1 (Philox noise per value; "
+                       "its seed advance included)")
     return res
 
 

@@ -304,6 +304,23 @@ size_t kvp_argmax_workspace_bytes(int32_t num_rows);
 int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t num_rows, int32_t vocab,
                     int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Sampling: for each row r with temperatures[r] > 0, out[r] = argmax_i of
+ * logits[r, i] / temperatures[r] + g, g = -log(-log(u)) (Gumbel-max: a sample of
+ * softmax(logits / T)); other rows (T <= 0 or NaN) take kvp_argmax_bf16's greedy index.
+ * u is the reference sampler's noise stream: Triton's tl.rand(seed, i + r * vocab), the
+ * first word of Philox4x32-10 for counter (i + r * vocab mod 2^32, 0, 0, 0) and the
+ * sign-extended *seed as key, scaled to [0, 1).  *seed is read on the device, so a
+ * captured graph draws new noise when the caller advances it between replays (the
+ * reference's Sampler adds 1 before every call).  temperatures: num_rows fp32.  Ties
+ * keep the first index; a NaN score counts as largest.  Replaces _sample_kernel and
+ * Sampler.forward's launch (kavor/layers/sampler.py:7-66).  Workspace as for
+ * kvp_argmax_bf16.
+ */
+int kvp_sample_bf16(const void* logits, int64_t row_stride, int32_t num_rows, int32_t vocab,
+                    const float* temperatures, const int32_t* seed, int64_t* out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -126,6 +126,12 @@ SIGNATURES: dict[str, tuple] = {
         _c_void_p,                        # out (int64)
         _c_void_p, _size_t, _c_void_p,    # workspace, workspace_bytes, stream
     ]),
+    "kvp_sample_bf16": (ctypes.c_int, [
+        _c_void_p, _i64, _i32, _i32,      # logits, row_stride, num_rows, vocab
+        _c_void_p, _c_void_p,             # temperatures (fp32), seed (int32, device)
+        _c_void_p,                        # out (int64)
+        _c_void_p, _size_t, _c_void_p,    # workspace, workspace_bytes, stream
+    ]),
 }
 
 _lock = threading.Lock()

@@ -6,7 +6,8 @@
 //                             appended to the paged cache (qwen3.py:79-89,
 //                             rotary_embedding.py:8-53, flash_attention_kvcache.py:10-34)
 //   silu_mul_kernel           SiLU(gate) * up (kavor/layers/activation.py:6-11)
-//   argmax_kernel             greedy token per logits row (kavor/layers/sampler.py:7-45, T = 0)
+//   argmax_kernel             greedy token per logits row, or a Gumbel-max sample per row
+//                             (kavor/layers/sampler.py:7-45)
 //
 // All are HBM / latency bound elementwise work: every thread moves 16-byte vectors of 8
 // bf16, reductions stay in registers (DPP inside a 16-lane row, lane swaps across rows),
@@ -261,6 +262,8 @@ struct ArgmaxParams {
   int segments;                 // workgroups per row (1: whole rows)
   int64_t* out;                 // whole rows: the index
   unsigned long long* keys;     // split rows: [row][segment] keys
+  const float* temperatures;    // sampling kernels: per row, <= 0 (or NaN) for greedy
+  const int32_t* seed;          // sampling kernels: the noise stream's seed (device)
 };
 
 // (v, i) beats (b, j): NaN above every number (as torch.argmax), then larger value, then
@@ -290,20 +293,57 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
   return (static_cast<unsigned long long>(ord) << 32) | (0xffffffffu - static_cast<u32>(i));
 }
 
+// ---- Gumbel-max sampling noise
+//
+// Row r draws token argmax_i(logit_i / T_r + g_ri), g = -log(-log(u)), u uniform in
+// [0, 1): a sample of softmax(logits / T_r) (the Gumbel-max trick).  u is the reference
+// sampler's stream (kavor/layers/sampler.py:34-38: tl.rand(seed, i + r * V)): the first
+// output word of Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers:
+// as easy as 1, 2, 3", SC 2011) for counter (i + r * V mod 2^32, 0, 0, 0) and key (the
+// low and high words of the sign-extended seed), turned into a float as
+// triton.language.random.uint_to_uniform_float does: the word as int32 x, x < 0 folded to
+// -x - 1, times 4.6566127342e-10.
+constexpr u32 kPhiloxMulA = 0xD2511F53u;
+constexpr u32 kPhiloxMulB = 0xCD9E8D57u;
+constexpr u32 kPhiloxWeylA = 0x9E3779B9u;
+constexpr u32 kPhiloxWeylB = 0xBB67AE85u;
+
+__device__ __forceinline__ u32 philox_word0(u32 ctr, u32 k0, u32 k1) {
+  u32 c0 = ctr, c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll
+  for (int round = 0; round < 10; ++round) {
+    const unsigned long long pa = static_cast<unsigned long long>(kPhiloxMulA) * c0;
+    const unsigned long long pb = static_cast<unsigned long long>(kPhiloxMulB) * c2;
+    c0 = static_cast<u32>(pb >> 32) ^ c1 ^ k0;
+    c2 = static_cast<u32>(pa >> 32) ^ c3 ^ k1;
+    c1 = static_cast<u32>(pb);
+    c3 = static_cast<u32>(pa);
+    k0 += kPhiloxWeylA;
+    k1 += kPhiloxWeylB;
+  }
+  return c0;
+}
+
+__device__ __forceinline__ float uniform_from_word(u32 w) {
+  const int x = static_cast<int>(w);
+  return static_cast<float>(x < 0 ? ~x : x) * 4.6566127342e-10f;
+}
+
+// The perturbed score of value f at counter ctr (the division and the logarithms are the
+// IEEE ones, as in the reference's kernel).
+__device__ __forceinline__ float gumbel_score(float f, float temp, u32 ctr, u32 k0, u32 k1) {
+  const float u = uniform_from_word(philox_word0(ctr, k0, k1));
+  return f / temp + (-logf(-logf(u)));
+}
+
 // Per chunk of 8 values a lane keeps, without branches, the NaN-propagating maximum over
 // its chunks, the chunk that first reached it and that chunk's raw bits; the index inside
 // the kept chunk is found once at the end.  A lane's chunks come in increasing index
 // order and only a strictly greater maximum (or a first NaN) replaces the kept chunk, so
-// ties keep the first occurrence.  The row segment is chunks [cbeg, cend); the
-// (vocab % 8)-value tail goes to the last segment.
-template <int THREADS, int BATCH, bool SPLIT>
-__global__ __launch_bounds__(THREADS) void argmax_kernel(ArgmaxParams p) {
-  const int r = SPLIT ? static_cast<int>(blockIdx.x) / p.segments : static_cast<int>(blockIdx.x);
-  const int seg = SPLIT ? static_cast<int>(blockIdx.x) - r * p.segments : 0;
-  const uint16_t* row = p.logits + r * p.row_stride;
-  const int nvec = p.vocab >> 3;
-  const int per = SPLIT ? (nvec + p.segments - 1) / p.segments : nvec;
-  const int cbeg = seg * per, cend = min(nvec, cbeg + per);
+// ties keep the first occurrence.  Chunks [cbeg, cend) of the row.  The result is this
+// lane's (value, index), index 0x7fffffff when it saw nothing.
+template <int THREADS, int BATCH>
+__device__ __forceinline__ void greedy_scan(const uint16_t* row, int cbeg, int cend, float& best, int& bi) {
   float cmax = -__builtin_inff();
   int bc = -1;
   uint4 bw = make_uint4(0, 0, 0, 0);
@@ -331,8 +371,8 @@ __global__ __launch_bounds__(THREADS) void argmax_kernel(ArgmaxParams p) {
   }
   // The first value of the kept chunk equal to its maximum (for NaN: the first NaN);
   // -0 and +0 compare equal, as in torch.argmax.
-  float best = -__builtin_inff();
-  int bi = 0x7fffffff;
+  best = -__builtin_inff();
+  bi = 0x7fffffff;
   if (bc >= 0) {
     float f[8];
     unpack8(bw, f);
@@ -343,10 +383,68 @@ __global__ __launch_bounds__(THREADS) void argmax_kernel(ArgmaxParams p) {
     best = cmax;
     bi = 8 * bc + e0;
   }
+}
+
+// The sampling counterpart: every value's Gumbel score, kept per lane with the same
+// order (NaN on top, then the larger score, then the smaller index).
+template <int THREADS, int BATCH>
+__device__ __forceinline__ void sample_scan(const uint16_t* row, int cbeg, int cend, float temp, u32 ctr0,
+                                            u32 k0, u32 k1, float& best, int& bi) {
+  best = -__builtin_inff();
+  bi = -1;
+  for (int c0 = cbeg + threadIdx.x; c0 < cend; c0 += THREADS * BATCH) {
+    uint4 w[BATCH];
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) w[u] = load16_nt(row + 8 * min(c0 + u * THREADS, cend - 1));
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int c = c0 + u * THREADS;
+      if (c >= cend) continue;
+      float f[8];
+      unpack8(w[u], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = gumbel_score(f[e], temp, ctr0 + static_cast<u32>(8 * c + e), k0, k1);
+        const bool up = bi < 0 || (v != v ? best == best : v > best);
+        best = up ? v : best;
+        bi = up ? 8 * c + e : bi;
+      }
+    }
+  }
+  if (bi < 0) bi = 0x7fffffff;
+}
+
+// Greedy argmax (SAMPLE false), or per-row Gumbel-max sampling (SAMPLE true: rows whose
+// temperature is not above 0 take the greedy scan).  Whole rows write the index; split
+// rows write one ordered key per segment for argmax_merge_kernel.  The row segment is
+// chunks [cbeg, cend); the (vocab % 8)-value tail goes to the last segment.
+template <int THREADS, int BATCH, bool SPLIT, bool SAMPLE>
+__global__ __launch_bounds__(THREADS) void argmax_kernel(ArgmaxParams p) {
+  const int r = SPLIT ? static_cast<int>(blockIdx.x) / p.segments : static_cast<int>(blockIdx.x);
+  const int seg = SPLIT ? static_cast<int>(blockIdx.x) - r * p.segments : 0;
+  const uint16_t* row = p.logits + r * p.row_stride;
+  const int nvec = p.vocab >> 3;
+  const int per = SPLIT ? (nvec + p.segments - 1) / p.segments : nvec;
+  const int cbeg = seg * per, cend = min(nvec, cbeg + per);
+  const float temp = SAMPLE ? p.temperatures[r] : 0.f;
+  const bool sampled = SAMPLE && temp > 0.f;
+  u32 k0 = 0, k1 = 0, ctr0 = 0;
+  float best;
+  int bi;
+  if (sampled) {
+    const int seed = *p.seed;
+    k0 = static_cast<u32>(seed);
+    k1 = seed < 0 ? 0xffffffffu : 0u;
+    ctr0 = static_cast<u32>(r) * static_cast<u32>(p.vocab);
+    sample_scan<THREADS, BATCH>(row, cbeg, cend, temp, ctr0, k0, k1, best, bi);
+  } else {
+    greedy_scan<THREADS, BATCH>(row, cbeg, cend, best, bi);
+  }
   const int tail = p.vocab - 8 * nvec;
   if ((!SPLIT || seg == p.segments - 1) && static_cast<int>(threadIdx.x) < tail) {
     const int i = 8 * nvec + threadIdx.x;
-    const float f = __uint_as_float(static_cast<u32>(row[i]) << 16);
+    float f = __uint_as_float(static_cast<u32>(row[i]) << 16);
+    if (sampled) f = gumbel_score(f, temp, ctr0 + static_cast<u32>(i), k0, k1);
     if (beats(f, i, best, bi)) { best = f; bi = i; }
   }
 #pragma unroll
@@ -537,35 +635,62 @@ extern "C" size_t kvp_argmax_workspace_bytes(int32_t num_rows) {
   return s == 1 ? 0 : static_cast<size_t>(num_rows) * s * sizeof(unsigned long long);
 }
 
-extern "C" int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t num_rows,
-                               int32_t vocab, int64_t* out, void* workspace, size_t workspace_bytes,
-                               void* stream) {
-  clear_error();
+// Checks shared by the argmax and sampling entry points.
+static int check_logits(const void* logits, int64_t row_stride, int32_t num_rows, int32_t vocab, const void* out,
+                        const void* workspace) {
   if (!logits || !out) return fail(KVP_EINVAL, "null pointer");
   if (num_rows < 0 || vocab < 1) return fail(KVP_EINVAL, "bad shape");
   if (!aligned16(logits) || !mult8(row_stride) || row_stride < vocab)
     return fail(KVP_EINVAL, "logits must be 16-byte aligned with a row stride >= vocab that is a "
                 "multiple of 8 elements");
-  if (num_rows == 0) return KVP_OK;
   if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 7u))
     return fail(KVP_EINVAL, "workspace must be 8-byte aligned");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  ArgmaxParams p{static_cast<const uint16_t*>(logits), row_stride, vocab, argmax_segments(num_rows), out,
-                 static_cast<unsigned long long*>(workspace)};
+  return KVP_OK;
+}
+
+template <bool SAMPLE>
+static int launch_argmax(ArgmaxParams p, int32_t num_rows, void* workspace, size_t workspace_bytes,
+                         hipStream_t s) {
+  p.segments = argmax_segments(num_rows);
+  p.keys = static_cast<unsigned long long*>(workspace);
   // Split rows need the caller's workspace; without one (or too small) rows stay whole.
   if (p.segments > 1 && workspace && workspace_bytes >= kvp_argmax_workspace_bytes(num_rows)) {
-    const int per = (vocab / 8 + p.segments - 1) / p.segments;  // chunks per segment
+    const int per = (p.vocab / 8 + p.segments - 1) / p.segments;  // chunks per segment
     if (per > 5 * kArgmaxSplitThreads)
-      hipLaunchKernelGGL((argmax_kernel<kArgmaxSplitThreads, 10, true>), dim3(num_rows * p.segments),
+      hipLaunchKernelGGL((argmax_kernel<kArgmaxSplitThreads, 10, true, SAMPLE>), dim3(num_rows * p.segments),
                          dim3(kArgmaxSplitThreads), 0, s, p);
     else
-      hipLaunchKernelGGL((argmax_kernel<kArgmaxSplitThreads, 5, true>), dim3(num_rows * p.segments),
+      hipLaunchKernelGGL((argmax_kernel<kArgmaxSplitThreads, 5, true, SAMPLE>), dim3(num_rows * p.segments),
                          dim3(kArgmaxSplitThreads), 0, s, p);
     hipLaunchKernelGGL(argmax_merge_kernel, dim3((num_rows + 255) / 256), dim3(256), 0, s, p, num_rows);
-    return launch_status("argmax_kernel (split rows)");
+    return launch_status(SAMPLE ? "sample kernel (split rows)" : "argmax_kernel (split rows)");
   }
   p.segments = 1;
-  hipLaunchKernelGGL((argmax_kernel<kArgmaxThreads, kArgmaxBatch, false>), dim3(num_rows), dim3(kArgmaxThreads), 0,
-                     s, p);
-  return launch_status("argmax_kernel");
+  hipLaunchKernelGGL((argmax_kernel<kArgmaxThreads, kArgmaxBatch, false, SAMPLE>), dim3(num_rows),
+                     dim3(kArgmaxThreads), 0, s, p);
+  return launch_status(SAMPLE ? "sample kernel" : "argmax_kernel");
+}
+
+extern "C" int kvp_argmax_bf16(const void* logits, int64_t row_stride, int32_t num_rows,
+                               int32_t vocab, int64_t* out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  clear_error();
+  const int rc = check_logits(logits, row_stride, num_rows, vocab, out, workspace);
+  if (rc != KVP_OK || num_rows == 0) return rc;
+  ArgmaxParams p{static_cast<const uint16_t*>(logits), row_stride, vocab, 1, out, nullptr, nullptr, nullptr};
+  return launch_argmax<false>(p, num_rows, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvp_sample_bf16(const void* logits, int64_t row_stride, int32_t num_rows, int32_t vocab,
+                               const float* temperatures, const int32_t* seed, int64_t* out,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const int rc = check_logits(logits, row_stride, num_rows, vocab, out, workspace);
+  if (rc != KVP_OK) return rc;
+  if (!temperatures || !seed) return fail(KVP_EINVAL, "null temperatures / seed");
+  if ((reinterpret_cast<uintptr_t>(temperatures) & 3u) || (reinterpret_cast<uintptr_t>(seed) & 3u))
+    return fail(KVP_EINVAL, "temperatures and seed must be 4-byte aligned");
+  if (num_rows == 0) return KVP_OK;
+  ArgmaxParams p{static_cast<const uint16_t*>(logits), row_stride, vocab, 1, out, nullptr, temperatures, seed};
+  return launch_argmax<true>(p, num_rows, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

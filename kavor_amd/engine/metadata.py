@@ -51,6 +51,7 @@ class DecodeMeta:
     slot_mapping: torch.Tensor
     context_lens: torch.Tensor
     block_tables: torch.Tensor
+    temperatures: torch.Tensor  # fp32, 0 for greedy rows and padding
 
 
 def _pinned_int32(n: int, pin: bool) -> torch.Tensor:
@@ -114,24 +115,27 @@ def prepare_prefill(seqs: list[Sequence], block_size: int, device, pin: bool = T
 
 
 class DecodeStaging:
-    """Fixed-layout decode metadata: [ids | positions | slots | context_lens | tables]
-    with `rows` rows and `width` block-table columns, in one pinned host buffer and one
-    device buffer.  `views(bs)` returns the device views of the first bs rows."""
+    """Fixed-layout decode metadata: [ids | positions | slots | context_lens |
+    temperatures (fp32 bits) | tables] with `rows` rows and `width` block-table columns,
+    in one pinned host buffer and one device buffer.  `views(bs)` returns the device
+    views of the first bs rows."""
 
     def __init__(self, rows: int, width: int, device, pin: bool = True):
         self.rows, self.width = rows, width
-        self.host = _pinned_int32(rows * (4 + width), pin)
+        self.host = _pinned_int32(rows * (5 + width), pin)
         self.h = self.host.numpy()
-        self.dev = torch.zeros(rows * (4 + width), dtype=torch.int32, device=device)
+        self.dev = torch.zeros(rows * (5 + width), dtype=torch.int32, device=device)
         self.h[:] = 0
         self._hf = [self.h[i * rows:(i + 1) * rows] for i in range(4)]
-        self._htab = self.h[4 * rows:].reshape(rows, width)
+        self._htemp = self.h[4 * rows:5 * rows].view(np.float32)
+        self._htab = self.h[5 * rows:].reshape(rows, width)
         self._df = [self.dev[i * rows:(i + 1) * rows] for i in range(4)]
-        self._dtab = self.dev[4 * rows:].view(rows, width)
+        self._dtemp = self.dev[4 * rows:5 * rows].view(torch.float32)
+        self._dtab = self.dev[5 * rows:].view(rows, width)
 
     def views(self, bs: int) -> DecodeMeta:
         ids, pos, slots, ctx = (t[:bs] for t in self._df)
-        return DecodeMeta(ids, pos, slots, ctx, self._dtab[:bs])
+        return DecodeMeta(ids, pos, slots, ctx, self._dtab[:bs], self._dtemp[:bs])
 
     def fill(self, seqs: list[Sequence], block_size: int, bs: int) -> None:
         """Writes the host rows for `seqs`, pads rows len(seqs)..bs-1, and copies the
@@ -168,6 +172,8 @@ class DecodeStaging:
         pos[n:bs] = 0
         slots[n:bs] = -1
         ctx[n:bs] = 0
+        self._htemp[:n] = np.fromiter((s.temperature for s in seqs), dtype=np.float32, count=n)
+        self._htemp[n:bs] = 0.0
         self.dev.copy_(self.host, non_blocking=True)
 
 
@@ -181,4 +187,5 @@ def decode_arrays(seqs: list[Sequence], block_size: int) -> dict:
     for i, s in enumerate(seqs):
         tab[i, len(s.block_table):] = -1
     return dict(input_ids=ids[:n], positions=pos[:n], slot_mapping=slots[:n],
-                context_lens=ctx[:n], block_tables=tab.reshape(n, w))
+                context_lens=ctx[:n], block_tables=tab.reshape(n, w),
+                temperatures=st._htemp[:n].copy())

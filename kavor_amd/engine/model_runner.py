@@ -12,8 +12,9 @@ the shared-memory control plane of :85-106 has nothing to do):
 - capture_cudagraph (:264-327): one hipGraph per batch size in
   [1, 2, 4, 8] + range(16, max_bs + 1, 16) (+ max_bs), sharing one memory pool,
   captured with all-zero metadata; as at tensor_parallel_size 1 there (:280-310), the
-  LM head and the greedy sampler are inside the graph, which leaves the tokens in a
-  persistent sampled_tokens buffer; the paged-decode workspace is reserved before
+  LM head and the sampler are inside the graph, which leaves the tokens in a
+  persistent sampled_tokens buffer (the rows' temperatures travel with the decode
+  metadata, the sampler's seed is a device buffer the graph advances); the paged-decode workspace is reserved before
   capture;
 - run / run_model (:213-262): prefill runs eagerly, decode replays the smallest graph
   that holds the batch, padding rows carry slot -1 and context length 0.
@@ -21,9 +22,8 @@ the shared-memory control plane of :85-106 has nothing to do):
 Per-step metadata travels in one host-to-device copy (kavor_amd.engine.metadata).  With
 the fused layers the prefill always carries block tables, because the model appends
 k / v before attention and attention reads the pages; with the drop-in caller order it
-carries them only when some sequence has cached tokens (:432-433).  An all-greedy decode batch reads its tokens from the
-graph's sampled_tokens; a batch with a temperature above 0 samples from the graph's
-logits after the replay (the reference's graph samples every temperature inside).
+carries them only when some sequence has cached tokens (:432-433).  A decode batch that a graph holds reads its tokens from the
+graph's sampled_tokens, at any temperature.
 """
 
 from __future__ import annotations
@@ -41,7 +41,7 @@ from kavor_amd.engine.qwen3 import Qwen3ForCausalLM, load_checkpoint_tensors
 from kavor_amd.engine.sampler import Sampler
 from kavor_amd.engine.sequence import Sequence
 from kavor_amd.layers.attention import reserve_decode_workspace
-from kavor_amd.layers.fused import argmax_workspace, greedy_argmax
+from kavor_amd.layers.fused import argmax_workspace
 from kavor_amd.utils.context import reset_context, set_context
 
 MAX_GRAPH_BATCH = 512
@@ -76,7 +76,7 @@ class ModelRunner:
             del tensors
         else:
             self.model.init_random(config.seed)
-        self.sampler = Sampler()
+        self.sampler = Sampler(self.device)
         self.pool = CachePool(self.model, self.spec.num_key_value_heads, self.spec.head_dim,
                               self.block_size)
         torch.cuda.synchronize()
@@ -130,7 +130,7 @@ class ModelRunner:
         try:
             zeros = torch.zeros(bs, dtype=torch.int32, device=dev)
             logits = self.model.compute_logits(self.model(zeros, zeros))
-            self.sampler(logits, torch.ones(bs, device=dev), False)
+            self.sampler(logits, torch.ones(bs, dtype=torch.float32, device=dev), False)
         finally:
             reset_context()
 
@@ -201,11 +201,12 @@ class ModelRunner:
                         block_tables=m.block_tables)
             try:
                 out, tok = self.logits_buf[:bs], self.sampled_buf[:bs]
-                greedy_argmax(self.model.compute_logits(self.model(m.input_ids, m.positions), out=out), out=tok)
+                self.sampler(self.model.compute_logits(self.model(m.input_ids, m.positions), out=out),
+                             m.temperatures, False, out=tok)
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, pool=pool):
-                    greedy_argmax(self.model.compute_logits(self.model(m.input_ids, m.positions), out=out),
-                                  out=tok)
+                    self.sampler(self.model.compute_logits(self.model(m.input_ids, m.positions), out=out),
+                                 m.temperatures, False, out=tok)
             finally:
                 reset_context()
             if pool is None:
@@ -228,27 +229,29 @@ class ModelRunner:
                             m.slot_mapping, None, m.block_tables)
                 logits = self.model.compute_logits(self.model(m.input_ids, m.positions))
             else:
-                logits, sampled = self._decode(seqs)
-                if all_greedy and sampled is not None:
-                    return sampled.tolist()  # the graph's LM head + greedy sampler
+                logits, sampled, t = self._decode(seqs)
+                if sampled is not None:
+                    return sampled.tolist()  # the graph's LM head + sampler
+                return self.sampler(logits, t, all_greedy).tolist()
             t = None if all_greedy else torch.tensor(temps, dtype=torch.float32).to(self.device, non_blocking=True)
             return self.sampler(logits, t, all_greedy).tolist()
         finally:
             reset_context()
 
-    def _decode(self, seqs: list[Sequence]) -> tuple[torch.Tensor, torch.Tensor | None]:
-        """Logits of a decode step, and the greedy tokens when a graph produced them."""
+    def _decode(self, seqs: list[Sequence]) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor]:
+        """Logits of a decode step, the sampled tokens when a graph produced them, and the
+        rows' temperatures on the device."""
         n = len(seqs)
         if self.graphs and n <= self.graph_bs[-1]:
             bs = next(b for b in self.graph_bs if b >= n)
             self.staging.fill(seqs, self.block_size, bs)
             self.graphs[bs].replay()
-            return self.logits_buf[:n], self.sampled_buf[:n]
+            return self.logits_buf[:n], self.sampled_buf[:n], self.staging.views(n).temperatures
         self.staging.fill(seqs, self.block_size, n)
         m = self.staging.views(n)
         set_context(False, slot_mapping=m.slot_mapping, context_lens=m.context_lens,
                     block_tables=m.block_tables)
-        return self.model.compute_logits(self.model(m.input_ids, m.positions)), None
+        return self.model.compute_logits(self.model(m.input_ids, m.positions)), None, m.temperatures
 
     def exit(self) -> None:
         self.graphs.clear()

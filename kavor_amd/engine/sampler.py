@@ -1,28 +1,29 @@
 """Token sampler (kavor/layers/sampler.py:7-66).
 
-Greedy rows (temperature 0) take the argmax of the logits, first index on ties, as
-torch.argmax and the reference kernel do; an all-greedy batch is one pass of the HIP
-argmax kernel (kvp_argmax_bf16).  Other rows draw with the Gumbel-max trick,
-argmax(logits / T + G) with G = -log(-log(U)), which samples softmax(logits / T)
-exactly; the random stream (torch's Philox generator) differs from the reference's, so
-sampled tokens at T > 0 are equal in distribution, not token for token.
+Every call advances a device seed by one and draws with it, as the reference's
+Sampler.forward does, so that a captured graph draws new noise on each replay.  Rows
+with a temperature above 0 take a Gumbel-max sample of softmax(logits / T) from the
+reference's noise stream (Philox4x32-10 words at offsets i + r * V, as Triton's tl.rand
+draws them); the others take the greedy index (first on ties).  Both run as one HIP
+kernel, kvp_sample_bf16; an all-greedy batch outside a graph takes the argmax kernel
+(kvp_argmax_bf16) directly.
 """
 
 from __future__ import annotations
 
 import torch
 
-from kavor_amd.layers.fused import greedy_argmax
+from kavor_amd.layers.fused import greedy_argmax, sample
 
 
 class Sampler:
 
-    def __call__(self, logits: torch.Tensor, temperatures: torch.Tensor, all_greedy: bool) -> torch.Tensor:
+    def __init__(self, device):
+        self.seed = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def __call__(self, logits: torch.Tensor, temperatures: torch.Tensor | None, all_greedy: bool,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
         if all_greedy:
-            return greedy_argmax(logits)
-        scores = logits.float()
-        t = temperatures.to(scores.device, torch.float32).unsqueeze(1)
-        u = torch.rand_like(scores).clamp_(min=1e-30, max=1.0 - 1e-7)
-        gumbel = -torch.log(-torch.log(u))
-        sampled = torch.where(t > 0, scores / t.clamp_min(1e-30) + gumbel, scores)
-        return sampled.argmax(dim=-1)
+            self.seed.add_(1)
+            return greedy_argmax(logits, out=out)
+        return sample(logits, temperatures, self.seed, out=out)

@@ -215,3 +215,33 @@ def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torc
                                out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(logits))
     check("kvp_argmax_bf16", rc)
     return out
+
+
+def sample(logits: torch.Tensor, temperatures: torch.Tensor, seed: torch.Tensor,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """int64 token per row: a Gumbel-max sample of softmax(logits / T) for rows with
+    T > 0, the greedy index for the others (kavor/layers/sampler.py:7-66).  seed is a
+    device int32 scalar that the call advances by one before drawing, as the reference's
+    Sampler.forward does, so that a captured graph draws new noise on every replay."""
+    _check_bf16("logits", logits)
+    if logits.dim() != 2:
+        raise ValueError("logits must be [num_rows, vocab]")
+    n = logits.shape[0]
+    if temperatures.dtype != torch.float32 or not temperatures.is_contiguous() or temperatures.numel() < n \
+            or temperatures.device != logits.device:
+        raise ValueError("temperatures must be a contiguous fp32 tensor on the logits' device, one per row")
+    if seed.dtype != torch.int32 or seed.numel() != 1 or seed.device != logits.device:
+        raise ValueError("seed must be a one-element int32 tensor on the logits' device")
+    if out is None:
+        out = torch.empty(n, dtype=torch.int64, device=logits.device)
+    if out.dtype != torch.int64 or not out.is_contiguous() or out.numel() != n:
+        raise ValueError("out must be a contiguous int64 tensor with one entry per row")
+    ws = argmax_workspace(logits.device)
+    need = lib().kvp_argmax_workspace_bytes(n)
+    if need > ws.numel():
+        raise RuntimeError(f"argmax workspace of {ws.numel()} bytes, {need} needed")
+    seed.add_(1)
+    rc = lib().kvp_sample_bf16(logits.data_ptr(), logits.stride(0), n, logits.shape[1], temperatures.data_ptr(),
+                               seed.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(logits))
+    check("kvp_sample_bf16", rc)
+    return out

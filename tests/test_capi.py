@@ -93,6 +93,43 @@ def test_noalloc_decode_rejects_bad_arguments_on_host():
     assert b"kvp_paged_decode_bf16_noalloc" in lib.kvp_last_error()
 
 
+def test_sample_rejects_bad_arguments_on_host():
+    lib = _lib.lib()
+    args = dict(logits=16, rs=151936, rows=4, vocab=151936, temps=16, seed=16, out=16, ws=None, wsb=0,
+                stream=None)
+
+    def call(**over):
+        return lib.kvp_sample_bf16(*dict(args, **over).values())
+
+    assert call(rows=0) == _lib.KVP_OK
+    assert call(temps=None) == _lib.KVP_EINVAL
+    assert call(seed=None) == _lib.KVP_EINVAL
+    assert call(seed=18) == _lib.KVP_EINVAL                  # not 4-byte aligned
+    assert call(rs=151937) == _lib.KVP_EINVAL                # stride not a multiple of 8
+    assert call(logits=8) == _lib.KVP_EINVAL                 # logits not 16-byte aligned
+    assert call(vocab=0) == _lib.KVP_EINVAL
+    assert call(ws=12) == _lib.KVP_EINVAL                    # workspace not 8-byte aligned
+
+
+def test_fused_decode_rejects_bad_arguments_on_host():
+    lib = _lib.lib()
+    args = dict(qkv=16, qkvs=4096, cs=16, maxpos=40960, qw=16, kw=16, eps=1e-6, kc=16, vc=16,
+                bstr=524288, sstr=1024, hstr=128, nblk=64, slots=16, bt=16, bts=16, ctx=16, b=4, hq=16, hkv=8,
+                d=128, bs=256, maxb=16, scale=0.088, out=16, os=2048, oh=128, ws=256, wsb=1 << 30, stream=None)
+
+    def call(**over):
+        return lib.kvp_paged_decode_fused_bf16(*dict(args, **over).values())
+
+    assert call(b=0) == _lib.KVP_OK
+    assert call(cs=None) == _lib.KVP_EINVAL
+    assert call(slots=None) == _lib.KVP_EINVAL
+    assert call(maxpos=0) == _lib.KVP_EINVAL
+    assert call(maxpos=1 << 23) == _lib.KVP_EINVAL           # table beyond 32-bit byte offsets
+    assert call(qkvs=3000) == _lib.KVP_EINVAL                # row shorter than (hq + 2 hkv) * 128
+    assert call(wsb=100) == _lib.KVP_EWORKSPACE
+    assert b"kvp_paged_decode_fused_bf16" in lib.kvp_last_error()
+
+
 def test_decode_workspace_size_formula():
     # 256-byte-aligned header (16 ints + a 4097-entry prefix table), then one state of 130
     # floats per query head for each of (ranges + sequences) slots; a launch has at most

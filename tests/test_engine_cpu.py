@@ -87,12 +87,13 @@ def test_prefill_and_decode_metadata_match_oracle(block_size):
 def test_decode_staging_pads_rows(block_size):
     from kavor_amd.engine.metadata import DecodeStaging
 
-    seqs = [Sequence(list(range(n)), SamplingParams()) for n in (1, 64, 65)]
+    seqs = [Sequence(list(range(n)), SamplingParams(temperature=t)) for n, t in ((1, 0.0), (64, 0.75), (65, 1.5))]
     for i, s in enumerate(seqs):
         s.block_table = list(range(10 * i, 10 * i + s.num_blocks))
     st = DecodeStaging(rows=8, width=4, device="cpu", pin=False)
     st.fill(seqs, block_size, 4)
     m = st.views(4)
+    assert m.temperatures.tolist() == [0.0, 0.75, 1.5, 0.0]
     assert m.context_lens.tolist() == [1, 64, 65, 0]
     assert m.slot_mapping.tolist() == [0, 10 * 64 + 63, 21 * 64 + 0, -1]
     assert m.positions.tolist() == [0, 63, 64, 0]

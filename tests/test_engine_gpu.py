@@ -14,6 +14,7 @@ import torch
 from kavor_amd.engine.llm_engine import LLM
 from kavor_amd.engine.qwen3 import Qwen3Spec
 from kavor_amd.sampling_params import SamplingParams
+from oracle import layers_oracle as lref
 from tests.engine_reference import check_greedy_tokens
 
 pytestmark = pytest.mark.gpu
@@ -58,6 +59,41 @@ def test_graph_decode_matches_reference(graph_llm, monkeypatch):
     assert graph_llm.model_runner.graphs, "decode graphs were not captured"
     assert any(not s["prefill"] for s in graph_llm.step_stats)
     _check(graph_llm, prompts, outs)
+
+
+def test_graph_decode_samples_at_temperature(graph_llm, monkeypatch):
+    """A batch mixing greedy and T > 0 rows decodes through the graphs, whose sampler
+    reads the rows' temperatures from the decode metadata and advances the device seed:
+    each step's tokens equal the oracle's Gumbel-max draw over that step's logits with
+    that seed (greedy rows: the argmax)."""
+    runner = graph_llm.model_runner
+    seen = []
+    decode = runner._decode
+
+    def spy(seqs):
+        logits, sampled, temps = decode(seqs)
+        if sampled is not None:
+            torch.cuda.synchronize()
+            seen.append((logits.cpu().clone(), sampled.cpu().clone(), temps.cpu().clone(),
+                         int(runner.sampler.seed.item())))
+        return logits, sampled, temps
+
+    monkeypatch.setattr(runner, "_decode", spy)
+    prompts = _prompts(7, [20, 33, 64, 5, 90])
+    sps = [SamplingParams(temperature=t, max_tokens=8, ignore_eos=True) for t in (0.0, 0.8, 1.0, 1.5, 0.0)]
+    outs = graph_llm.generate(prompts, sps)
+    assert [len(o["token_ids"]) for o in outs] == [8] * 5
+    assert len(seen) >= 5
+    for logits, sampled, temps, seed in seen:
+        t = temps.numpy()
+        scores = lref.gumbel_scores(logits, t, seed)
+        want = lref.first_argmax(scores)
+        for r in range(len(want)):
+            if sampled[r].item() != want[r]:
+                a, b = scores[r, sampled[r].item()], scores[r, want[r]]
+                assert abs(a - b) <= 4e-7 * max(1.0, abs(b)), (r, a, b)
+    # the running order is the submission order
+    assert np.allclose(seen[0][2].numpy(), [0.0, 0.8, 1.0, 1.5, 0.0])
 
 
 def test_prefix_cache_hit_reuses_pages(graph_llm):
