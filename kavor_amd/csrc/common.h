@@ -135,4 +135,41 @@ __device__ __forceinline__ void norm_rope_head(float (&x)[8], const float (&w)[8
 // exp2(m_old - m_new) never evaluates (-inf) - (-inf).
 constexpr float kMaxFloor = -1.0e30f;
 
+// ---- direct-to-LDS buffer loads
+//
+// buffer_load_dwordx4 ... lds: lane l of the wave writes the 16 bytes it loads at the LDS
+// address in M0 + 16 l; the load is counted by vmcnt like any vector load, and vector
+// memory operations complete in issue order.  The global_load_lds form is not used: the
+// compiler treats it as a flat access to both memories and, while one is in flight,
+// waits for every outstanding load at the next use of any loaded register.  Buffer loads
+// are range-checked against the resource's size (out-of-range lanes read zeros).  The
+// compiler does not order later LDS reads of the destination after these loads, so the
+// kernels wait explicitly (wait_vmem) before reading what they filled.
+typedef int32_t BufferRsrc __attribute__((ext_vector_type(4)));
+__device__ void raw_buffer_load_lds(BufferRsrc rsrc, __attribute__((address_space(3))) void* lds, int size,
+                                    int voffset, int soffset, int offset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+// Buffer resource over `bytes` bytes at `base` (stride 0, raw byte offsets).
+__device__ __forceinline__ BufferRsrc buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  BufferRsrc r;
+  r.x = static_cast<int32_t>(static_cast<uint32_t>(a));
+  r.y = static_cast<int32_t>((a >> 32) & 0xffffu);
+  r.z = static_cast<int32_t>(bytes);
+  r.w = 0x00020000;  // gfx9 word 3: 32-bit data format, no swizzle
+  return r;
+}
+
+// 16 bytes at byte offset voffset of the resource into LDS at lds + 16 * lane.
+__device__ __forceinline__ void lds_dma16(BufferRsrc rsrc, int voffset, void* lds) {
+  raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
+// Waits until at most N vector memory operations of the wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 }  // namespace kvp

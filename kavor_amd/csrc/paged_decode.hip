@@ -334,10 +334,7 @@ __device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh
 // step S - 1, after the K/V loads of step S and before those of step S + 1 (2 NL loads);
 // vector memory operations complete in issue order, so an explicit wait that leaves at
 // most 2 NL of them in flight covers it.  The compiler's own tracking of direct-to-LDS
-// loads does not order these reads, hence the explicit wait.  The global_load_lds form
-// is avoided: the compiler treats it as a flat access to both memories and waits for
-// every outstanding load at the next use of any loaded register.  Buffer loads are
-// range-checked against the resource's size by the hardware.  The token's position is
+// loads does not order these reads, hence the explicit wait.  The token's position is
 // context_lens[b] - 1.
 constexpr int kFzRow = 512;  // bytes: one cos/sin row, 128 fp32
 constexpr int kFzNew = 1024;  // new token: cos/sin row | raw k head | raw v head
@@ -346,33 +343,6 @@ struct FzSize {  // q of a sequence: cos/sin row | G raw q heads, in 1 KiB loads
   static constexpr int kLoads = (kFzRow + G * 256 + 1023) / 1024;
   static constexpr int kBytes = kLoads * 1024;
 };
-
-typedef int32_t BufferRsrc __attribute__((ext_vector_type(4)));
-__device__ void raw_buffer_load_lds(BufferRsrc rsrc, __attribute__((address_space(3))) void* lds, int size,
-                                    int voffset, int soffset, int offset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.lds");
-
-// Buffer resource over `bytes` bytes at `base` (stride 0, raw byte offsets).
-__device__ __forceinline__ BufferRsrc buffer_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  BufferRsrc r;
-  r.x = static_cast<int32_t>(static_cast<uint32_t>(a));
-  r.y = static_cast<int32_t>((a >> 32) & 0xffffu);
-  r.z = static_cast<int32_t>(bytes);
-  r.w = 0x00020000;  // gfx9 word 3: 32-bit data format, no swizzle
-  return r;
-}
-
-// Waits until at most N vector memory operations of the wave are in flight.
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// 16 bytes at byte offset voffset of the resource into LDS region + 16 * lane.
-__device__ __forceinline__ void lds_dma16(BufferRsrc rsrc, int voffset, char* region) {
-  raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)region, 16, voffset, 0, 0, 0);
-}
 
 __device__ __forceinline__ BufferRsrc cos_sin_rsrc(const DecodeParams& p) {
   return buffer_rsrc(p.cos_sin, static_cast<uint32_t>(p.max_position) * kFzRow);

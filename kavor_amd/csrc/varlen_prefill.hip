@@ -12,8 +12,9 @@
 //   and all G query heads
 //   of that kv head: 128 "rows" = 128/G query tokens x G heads, row rho = tok*G + g, so a
 //   staged K/V tile feeds G heads.  Wave w owns rows [32w, 32w+32).
-//   Per 64-key tile the workgroup stages K and V row-major in LDS (double-buffered, one
-//   barrier per tile; the next tile's global loads are in flight during the MFMAs),
+//   Per 64-key tile K and V go from memory straight into LDS with direct-to-LDS buffer
+//   loads (double-buffered, one barrier per tile; the next tile's loads are in flight
+//   during the MFMAs, and no register holds them),
 //   then each wave computes S^T = K Q^T (M = 64 keys, N = 32 rows, K-dim = 128) and
 //   O^T += V^T P^T (M = 128 dims, N = 32 rows, K-dim = 64 keys), reading the V^T operand
 //   with the gfx950 LDS transpose load (ds_read_b64_tr_b16).  With the transposed
@@ -37,18 +38,14 @@ namespace kvp {
 constexpr int kPrefillHeadDim = 128;
 constexpr int kPrefillWaves = 4;
 constexpr int kPrefillThreads = 64 * kPrefillWaves;
-// 16-byte chunks of one 64-key tile (64 keys x 16 chunks) per thread, per tensor
-constexpr int kStageIters = 64 * 16 / kPrefillThreads;
 constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows (token x head) per workgroup
 constexpr int kKeyTile = 64;
-constexpr int kKStride = kPrefillHeadDim + 8;  // LDS row pitch of the K tile (bf16)
 constexpr int kXcdGroup = 2;  // neighbouring query tiles of one (sequence, kv head) per XCD
-constexpr int kVStride = kPrefillHeadDim + 32;  // LDS row pitch of the V tile (bf16): 80 dwords keeps the transposed reads conflict-free
-// Sequences per launch: their lengths and starts (8 bytes each) are staged in the idle
-// K and V tile buffers before the first tile; larger batches run as consecutive launches.
-constexpr int kMaxPrefillSeqs = 4096;
-static_assert(2 * kKeyTile * kKStride * 2 >= kMaxPrefillSeqs * 8, "lengths must fit the K buffers");
-static_assert(2 * kKeyTile * kVStride * 2 >= kMaxPrefillSeqs * 8, "starts must fit the V buffers");
+// Sequences per launch: their lengths and starts (8 bytes each) are staged in an idle K
+// and an idle V tile buffer before the first tile; larger batches run as consecutive
+// launches.
+constexpr int kMaxPrefillSeqs = 2048;
+static_assert(kKeyTile * kPrefillHeadDim * 2 >= kMaxPrefillSeqs * 8, "lengths must fit one tile buffer");
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -105,6 +102,7 @@ __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
 // barriers are independent, so one's MFMAs overlap the other's softmax (measured
 // 1.45 -> 0.83 ms on the prefix-cached prefill workload vs one 4-wave workgroup per CU,
 // 0.97 ms with one 8-wave workgroup).
+
 template <int G, bool PAGED, bool CAUSAL>
 __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2))) void varlen_prefill_kernel(const PrefillParams p) {
   constexpr int D = kPrefillHeadDim;
@@ -132,13 +130,15 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
 
   // Two buffers of the K and V tiles (row-major, padded rows): tile i+1 is written while
   // other waves may still read tile i.
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKeyTile * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kKeyTile * kVStride];
-  __shared__ int s_bad;
+  __shared__ __attribute__((aligned(16))) uint16_t s_k0[kKeyTile * kPrefillHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t s_k1[kKeyTile * kPrefillHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v0[kKeyTile * kPrefillHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v1[kKeyTile * kPrefillHeadDim];
+
   // Before the first K/V tile is staged, the K buffers hold every sequence's
   // (query length, key length) and the V buffers its (query start, key start).
-  int2* s_len = reinterpret_cast<int2*>(&s_k[0][0]);
-  int2* s_start = reinterpret_cast<int2*>(&s_v[0][0]);
+  int2* s_len = reinterpret_cast<int2*>(&s_k0[0]);
+  int2* s_start = reinterpret_cast<int2*>(&s_v0[0]);
   const int J = p.pair_slots;  // tile pairs per (sequence, kv head) the grid covers
 
   // Units of sequence (ql, kl) whose first tile needs at least L key tiles.  Tile i of
@@ -180,7 +180,6 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     s_len[i] = make_int2(q1s - q0s, k1s - k0s);
     s_start[i] = make_int2(q0s, k0s);
   }
-  if (tid == 0) s_bad = 0;  // sticky for the workgroup: one sequence, one block table
   __syncthreads();
 
   // Rank r in the order of decreasing cost (ties: sequence, kv head, unit).  Every wave
@@ -252,12 +251,16 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   int bt_lane = -1;
   if (PAGED && lane < p.max_blocks) bt_lane = p.block_tables[s * p.bt_stride + lane];
 
-  // Thread t stages 16-byte chunk (t % 16) of keys t/16 + (threads/16)*u of a 64-key tile;
-  // keys past the context are staged as zeros.
-  const int chunk = tid & 15;
-  auto load_tile = [&](int kv0, uint4 (&kc)[kStageIters], uint4 (&vc)[kStageIters]) {
-    int64_t kbase = 0, vbase = 0;
-    bool blk_ok = true;
+  // Tiles go from memory straight into LDS (lds_dma16: lane l of a wave writes 16 bytes
+  // at the instruction's LDS base + 16 l), through a buffer resource over the tile's 64
+  // key rows (a tile never crosses a page: block sizes are multiples of 64).  Wave w, instruction i
+  // fills rows 4(4i + w) .. +3 of the unpadded [64 keys][128 dims] tile; lane l covers
+  // row 4(4i + w) + l/16 and physical chunk l % 16, which holds logical chunk
+  // pc ^ swz(row): K rows are swizzled by (row & 15), V rows by 4 (row & 3).  Keys past
+  // the context are clamped onto its last key; their scores are masked.  Every wave of the
+  // workgroup looks up the same block ids, so `bad` is uniform over the workgroup.
+  auto issue_k = [&](int kv0, uint16_t* dk) __attribute__((always_inline)) {
+    int64_t kbase = 0;
     if (PAGED) {
       const int lblk = kv0 / p.block_size;
       const int w = lblk >> 6;
@@ -267,34 +270,53 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       }
       int blk = lblk < p.max_blocks ? __builtin_amdgcn_readlane(bt_lane, lblk & 63) : -1;
       if (blk < 0 || blk >= p.num_cache_blocks) {
-        blk_ok = false;
+        bad = true;
         blk = 0;
       }
-      const int off = kv0 - lblk * p.block_size;
-      kbase = static_cast<int64_t>(blk) * p.k_blk_stride + static_cast<int64_t>(off) * p.k_tok_stride;
-      vbase = static_cast<int64_t>(blk) * p.v_blk_stride + static_cast<int64_t>(off) * p.v_tok_stride;
+      kbase = static_cast<int64_t>(blk) * p.k_blk_stride + static_cast<int64_t>(kv0 - lblk * p.block_size) * p.k_tok_stride;
     } else {
       kbase = static_cast<int64_t>(k_start + kv0) * p.k_tok_stride;
+    }
+    const uint16_t* kb = p.k + kbase + static_cast<int64_t>(kvh) * p.k_head_stride;
+    const BufferRsrc krs = buffer_rsrc(kb, static_cast<uint32_t>(kKeyTile * p.k_tok_stride * 2));
+    const int last = klen - 1 - kv0;
+    const int pc = lane & 15;
+#pragma unroll
+    for (int i = 0; i < kKeyTile / 4 / kPrefillWaves; ++i) {
+      const int r0 = 4 * (kPrefillWaves * i + wave);
+      const int r = r0 + (lane >> 4);
+      const int key = min(r, last);
+      lds_dma16(krs, (key * static_cast<int>(p.k_tok_stride) + 8 * (pc ^ (r & 15))) * 2, &dk[r0 * kPrefillHeadDim]);
+    }
+  };
+  auto issue_v = [&](int kv0, uint16_t* dv) __attribute__((always_inline)) {
+    int64_t vbase = 0;
+    if (PAGED) {
+      const int lblk = kv0 / p.block_size;
+      const int w = lblk >> 6;
+      if (w != bt_win) {  // uniform
+        bt_lane = 64 * w + lane < p.max_blocks ? p.block_tables[s * p.bt_stride + 64 * w + lane] : -1;
+        bt_win = w;
+      }
+      int blk = lblk < p.max_blocks ? __builtin_amdgcn_readlane(bt_lane, lblk & 63) : -1;
+      if (blk < 0 || blk >= p.num_cache_blocks) {
+        bad = true;
+        blk = 0;
+      }
+      vbase = static_cast<int64_t>(blk) * p.v_blk_stride + static_cast<int64_t>(kv0 - lblk * p.block_size) * p.v_tok_stride;
+    } else {
       vbase = static_cast<int64_t>(k_start + kv0) * p.v_tok_stride;
     }
-    if (!blk_ok) bad = true;
-    kbase += static_cast<int64_t>(kvh) * p.k_head_stride + 8 * chunk;
-    vbase += static_cast<int64_t>(kvh) * p.v_head_stride + 8 * chunk;
-    if (kv0 + kKeyTile <= klen && blk_ok) {  // whole tile inside the context (uniform)
+    const uint16_t* vb = p.v + vbase + static_cast<int64_t>(kvh) * p.v_head_stride;
+    const BufferRsrc vrs = buffer_rsrc(vb, static_cast<uint32_t>(kKeyTile * p.v_tok_stride * 2));
+    const int last = klen - 1 - kv0;
+    const int pc = lane & 15;
 #pragma unroll
-      for (int u = 0; u < kStageIters; ++u) {
-        const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
-        kc[u] = *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride);
-        vc[u] = *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < kStageIters; ++u) {
-        const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
-        const bool ok = kv0 + key < klen && blk_ok;
-        kc[u] = ok ? *reinterpret_cast<const uint4*>(p.k + kbase + key * p.k_tok_stride) : make_uint4(0, 0, 0, 0);
-        vc[u] = ok ? *reinterpret_cast<const uint4*>(p.v + vbase + key * p.v_tok_stride) : make_uint4(0, 0, 0, 0);
-      }
+    for (int i = 0; i < kKeyTile / 4 / kPrefillWaves; ++i) {
+      const int r0 = 4 * (kPrefillWaves * i + wave);
+      const int r = r0 + (lane >> 4);
+      const int key = min(r, last);
+      lds_dma16(vrs, (key * static_cast<int>(p.v_tok_stride) + 8 * (pc ^ (4 * (r & 3)))) * 2, &dv[r0 * kPrefillHeadDim]);
     }
   };
 
@@ -305,6 +327,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   // keys 4hf + e, which is the key order of this lane's P registers.
   const int tr_key = 4 * hf + ((lane & 15) >> 2);
   const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int tr_chunk = tr_dim >> 3, tr_sub = tr_dim & 7;
 
   const int ntiles_seq = (qlen + TOK - 1) / TOK;
   // This unit's tile pairs jj, jj + J, jj + 2J, ... counted from the last tile (more
@@ -344,20 +367,21 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     // smallest row_limit over this wave's rows (its first query token)
     const int wave_min_limit = CAUSAL ? q0 + (32 * wave) / G + diag : klen - 1;
 
-    uint4 kc[kStageIters], vc[kStageIters];
-    if (nkv > 0) load_tile(0, kc, vc);
-    for (int it = 0; it < nkv; ++it) {
+    if (nkv > 0) {
+      issue_k(0, s_k0);
+      issue_v(0, s_v0);
+    }
+    auto tile_step = [&](int it, const uint16_t* sk, const uint16_t* sv, uint16_t* nk, uint16_t* nv)
+                         __attribute__((always_inline)) {
       const int kv0 = it * kKeyTile;
-      uint16_t* sk = s_k[it & 1];
-      uint16_t* sv = s_v[it & 1];
-#pragma unroll
-      for (int u = 0; u < kStageIters; ++u) {
-        const int key = (tid >> 4) + (kPrefillThreads / 16) * u;
-        *reinterpret_cast<uint4*>(&sk[key * kKStride + 8 * chunk]) = kc[u];
-        *reinterpret_cast<uint4*>(&sv[key * kVStride + 8 * chunk]) = vc[u];
+      // this wave's share of tile `it` has landed; after the barrier every wave's has, and
+      // every wave is done with tile it-1's buffers
+      wait_vmem<0>();
+      __syncthreads();
+      if (it + 1 < nkv) {  // in flight during the MFMAs
+        issue_k(kv0 + kKeyTile, nk);
+        issue_v(kv0 + kKeyTile, nv);
       }
-      __syncthreads();  // tile `it` staged; every wave is done with tile it-1's buffer
-      if (it + 1 < nkv) load_tile(kv0 + kKeyTile, kc, vc);  // in flight during the MFMAs
 
       // ---- S^T = K Q^T : two 32-key blocks, lane holds keys of its own query row
       f32x16_t sacc[2];
@@ -373,16 +397,17 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         // ring of four K fragments keeps four LDS reads in flight ahead of the MFMAs
         // (the compiler's own order waited on a fresh read before every other MFMA;
         // 0.459 -> 0.456 ms on the prefix-cached 32-sequence workload, same bits).
-        const uint16_t* krow = &sk[n * kKStride + 8 * hf];
+        const uint16_t* krow = &sk[n * kPrefillHeadDim];
+        const int ksw = n & 15;
         uint4 ka[4];
 #pragma unroll
         for (int st = 0; st < 4; ++st)
-          ka[st] = *reinterpret_cast<const uint4*>(krow + (st & 1) * 32 * kKStride + 16 * (st >> 1));
+          ka[st] = *reinterpret_cast<const uint4*>(krow + (st & 1) * 32 * kPrefillHeadDim + 8 * ((2 * (st >> 1) + hf) ^ ksw));
 #pragma unroll
         for (int st = 0; st < 2 * (D / 16); ++st) {
           sacc[st & 1] = mfma32(ka[st & 3], qreg[st >> 1], sacc[st & 1]);
           if (st + 4 < 2 * (D / 16))
-            ka[st & 3] = *reinterpret_cast<const uint4*>(krow + ((st + 4) & 1) * 32 * kKStride + 16 * ((st + 4) >> 1));
+            ka[st & 3] = *reinterpret_cast<const uint4*>(krow + ((st + 4) & 1) * 32 * kPrefillHeadDim + 8 * ((2 * ((st + 4) >> 1) + hf) ^ ksw));
         }
         // Pin that order: 4 LDS reads, then (MFMA, LDS read) x 12, then the last 4 MFMAs.
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
@@ -455,9 +480,9 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         auto read_v = [&](int kk, uint4 (&dst)[D / 32]) __attribute__((always_inline)) {
 #pragma unroll
           for (int mb = 0; mb < D / 32; ++mb) {
-            const uint16_t* vp = &sv[(16 * kk + tr_key) * kVStride + 32 * mb + tr_dim];
+            const uint16_t* vp = &sv[(16 * kk + tr_key) * kPrefillHeadDim + 8 * ((4 * mb + tr_chunk) ^ (lane & 12)) + tr_sub];
             const uint2 lo = lds_read_tr16(vp);
-            const uint2 hi = lds_read_tr16(vp + 8 * kVStride);
+            const uint2 hi = lds_read_tr16(vp + 8 * kPrefillHeadDim);
             dst[mb] = make_uint4(lo.x, lo.y, hi.x, hi.y);
           }
         };
@@ -481,15 +506,17 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         }
         __builtin_amdgcn_sched_group_barrier(0x008, D / 32, 0);
       }
+    };
+    for (int it = 0; it < nkv; it += 2) {
+      tile_step(it, s_k0, s_v0, s_k1, s_v1);
+      if (it + 1 < nkv) tile_step(it + 1, s_k1, s_v1, s_k0, s_v0);
     }
     __builtin_amdgcn_s_setprio(0);
-    __syncthreads();
-    if (bad) s_bad = 1;
-    __syncthreads();
+    __syncthreads();  // every wave is done with the tile buffers (the next unit restages them)
 
     // ---- write O: lane holds dims 32mb + 8(j/4) + 4hf + (j%4) of its query row
     if (row_valid) {
-      const bool poisoned = s_bad != 0;
+      const bool poisoned = bad;
       const float inv = poisoned ? NAN : (l_run > 0.f ? 1.f / l_run : 0.f);
       uint16_t* op = p.out + static_cast<int64_t>(q_start + qi) * p.o_tok_stride +
                      static_cast<int64_t>(kvh * G + g) * p.o_head_stride;
