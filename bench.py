@@ -794,7 +794,8 @@ PROFILE_KERNELS = [
     ("qk_norm_rope_append_16384tok", "void kvp::(anonymous namespace)::qk_norm_rope_append_kernel<4>", "qk_norm_rope_append"),
     ("add_rmsnorm_16384x1024", "void kvp::(anonymous namespace)::rmsnorm_kernel<64, 2>", "add_rmsnorm"),
     ("silu_mul_16384x3072", "kvp::(anonymous namespace)::silu_mul_kernel", "silu_mul"),
-    ("argmax_256x151936", "void kvp::(anonymous namespace)::argmax_kernel<1024, 3, false>", "argmax"),
+    ("argmax_256x151936", "void kvp::(anonymous namespace)::argmax_kernel<1024, 3, false, false>", "argmax"),
+    ("sample_256x151936", "void kvp::(anonymous namespace)::argmax_kernel<1024, 3, false, true>", "sample_t1"),
 ]
 
 
@@ -861,6 +862,9 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         else:
             lines += [f"- algorithmic bytes: {algo[key]} -> {algo[key] / med_us / 1e3:.1f} GB/s at the median "
                       f"duration ({algo[key] / med_us / 1e3 / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)"]
+        if key == "sample_t1":
+            lines += ["- bound by the Philox noise arithmetic (ten rounds of two 32x32->64-bit products per "
+                      "value, VALU), not by HBM: T = 1 on every row"]
         lines += [f"- FETCH_SIZE calibration: 1 GiB copy reads {copy_f:.1f} KiB -> scale {f_scale:.4f}; "
                   f"WRITE_SIZE: 1 GiB copy writes {copy_w:.1f} KiB -> scale {w_scale:.4f}",
                   f"- HBM traffic per dispatch (scaled): read {statistics.mean(fetch):.0f} B, "
