@@ -124,6 +124,25 @@ def time_launches(fn, steps: int, warmup: int):
     return start.elapsed_time(end) / steps
 
 
+def time_median(fn, steps: int, warmup: int, groups: int = 5):
+    """Median over `groups` groups of HIP-event-timed launches (steps in all), in ms per
+    call: one slow group (a clock dip on a long kernel) does not move the figure."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    per = max(1, steps // groups)
+    times = []
+    for _ in range(groups):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(per):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / per)
+    return statistics.median(times)
+
+
 def warm_for(fn, seconds: float) -> None:
     """Runs fn until `seconds` of wall time have passed (synchronising every 10 calls):
     the clocks of a part that was idle take a few hundred milliseconds of full load to
@@ -422,8 +441,8 @@ def bench_prefill(dev, steps, warmup, dense: bool = False):
     def step():
         varlen_prefill(q, kc, vc, max(qlens), cq, max(klens), ck, SCALE, causal=True, block_table=bt, out=out)
 
-    warm_for(step, 0.3)
-    ms = time_launches(step, steps, warmup)
+    warm_for(step, 0.5)
+    ms = time_median(step, steps, warmup)
     flops = prefill_flops(cq.cpu().tolist(), ck.cpu().tolist(), hq, D)
     return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9)
 

@@ -252,3 +252,39 @@ def test_separate_decode_launches_match_reference(cuda_device):
     finally:
         llm.exit()
 
+
+
+def test_copy_blocks_on_device_pages_feed_the_decode(cuda_device):
+    """copy_blocks (cache_pool.py:142-149) on a device pool: the copied pages equal their
+    sources byte for byte in every layer, the other pages keep their bytes, and paged
+    decode over a block table that names the copies returns the same bits as over the
+    originals."""
+    from kavor_amd.engine.cache_pool import CachePool
+    from kavor_amd.engine.qwen3 import Qwen3ForCausalLM
+    from kavor_amd.layers.attention import paged_decode
+    from oracle import kvpath_oracle as ref
+
+    model = Qwen3ForCausalLM(TINY, cuda_device)
+    hkv, D, bs = TINY.num_key_value_heads, TINY.head_dim, 64
+    pool = CachePool(model, hkv, D, block_size=bs)
+    pool.allocate(16, cuda_device)
+    g = torch.Generator(device=cuda_device).manual_seed(3)
+    pool.pools.view(torch.bfloat16).copy_(torch.randn(pool.pools.view(torch.bfloat16).shape, generator=g,
+                                                      device=cuda_device, dtype=torch.bfloat16))
+    before = pool.pools.clone()
+    src, dst = [3, 7, 1], [10, 12, 14]
+    pool.copy_blocks(src, dst)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.pools[:, dst], before[:, src])
+    others = [i for i in range(16) if i not in dst]
+    assert torch.equal(pool.pools[:, others], before[:, others])
+    kc, vc = ref.page_views(pool.pools[0], bs, hkv, D)
+    q = torch.randn(2, TINY.num_attention_heads, D, generator=g, device=cuda_device, dtype=torch.bfloat16)
+    ctx = torch.tensor([150, 100], dtype=torch.int32, device=cuda_device)
+    bt_src = torch.tensor([[3, 7, 1], [1, 3, -1]], dtype=torch.int32, device=cuda_device)
+    bt_dst = torch.tensor([[10, 12, 14], [14, 10, -1]], dtype=torch.int32, device=cuda_device)
+    a = paged_decode(q, kc, vc, ctx, bt_src, D ** -0.5).clone()
+    b = paged_decode(q, kc, vc, ctx, bt_dst, D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.isfinite(a.float()).all()
