@@ -461,8 +461,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(const Deco
   constexpr int kMinSteps = kMinRangeTokens / STEP;
   __shared__ int s_cum[kMaxSeqsPerLaunch + 1];
   __shared__ int s_part[kDecodeThreads];
-  // fused scratch, per wave: norm weights; q inputs and new-token inputs for each of the
-  // two copies of the step loop (distinct objects: see the fused helpers)
+  // fused scratch, per wave: norm weights; q inputs and new-token inputs, one region of
+  // each per copy of the unrolled step loop (see the fused helpers)
   constexpr int kFzWaves = FUSED ? kDecodeWaves : 1;
   __shared__ __attribute__((aligned(16))) char s_fw[kFzWaves][1024];
   __shared__ __attribute__((aligned(16))) char s_fq0[kFzWaves][FUSED ? FzSize<G>::kBytes : 16];
