@@ -316,14 +316,22 @@ constexpr u32 kPhiloxMulB = 0xCD9E8D57u;
 constexpr u32 kPhiloxWeylA = 0x9E3779B9u;
 constexpr u32 kPhiloxWeylB = 0xBB67AE85u;
 
+// a ^ b ^ k in one instruction: gfx950's three-input bit operation with the XOR truth table
+// (0x96); the compiler emits two v_xor_b32 here.
+__device__ __forceinline__ u32 xor3(u32 a, u32 b, u32 k) {
+  u32 r;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+  return r;
+}
+
 __device__ __forceinline__ u32 philox_word0(u32 ctr, u32 k0, u32 k1) {
   u32 c0 = ctr, c1 = 0, c2 = 0, c3 = 0;
 #pragma unroll
   for (int round = 0; round < 10; ++round) {
     const unsigned long long pa = static_cast<unsigned long long>(kPhiloxMulA) * c0;
     const unsigned long long pb = static_cast<unsigned long long>(kPhiloxMulB) * c2;
-    c0 = static_cast<u32>(pb >> 32) ^ c1 ^ k0;
-    c2 = static_cast<u32>(pa >> 32) ^ c3 ^ k1;
+    c0 = xor3(static_cast<u32>(pb >> 32), c1, k0);
+    c2 = xor3(static_cast<u32>(pa >> 32), c3, k1);
     c1 = static_cast<u32>(pb);
     c3 = static_cast<u32>(pa);
     k0 += kPhiloxWeylA;
