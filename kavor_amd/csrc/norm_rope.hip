@@ -352,6 +352,36 @@ __device__ __forceinline__ float gumbel_score(float f, float temp, u32 ctr, u32 
   return f / temp + (-logf(-logf(u)));
 }
 
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_key(unsigned long long k) {
+  const u32 lo = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<u32>(k)), CTRL, 0xf, 0xf, false));
+  const u32 hi = static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<u32>(k >> 32)), CTRL, 0xf, 0xf, false));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long max_key(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+// Largest key over the caller's 16-lane DPP row (every lane of the row gets it).
+__device__ __forceinline__ unsigned long long row16_max_key(unsigned long long k) {
+  k = max_key(k, dpp_key<kDppQuadXor1>(k));
+  k = max_key(k, dpp_key<kDppQuadXor2>(k));
+  k = max_key(k, dpp_key<kDppRowHalfMirror>(k));
+  k = max_key(k, dpp_key<kDppRowMirror>(k));
+  return k;
+}
+// Largest key over the wave (wave-uniform result): the four rows' maxima read by lane.
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k) {
+  k = row16_max_key(k);
+  unsigned long long m = 0;
+#pragma unroll
+  for (int row = 0; row < 4; ++row) {
+    const u32 lo = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(k)), 16 * row));
+    const u32 hi = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(k >> 32)), 16 * row));
+    m = max_key(m, (static_cast<unsigned long long>(hi) << 32) | lo);
+  }
+  return m;
+}
+
 // Per chunk of 8 values a lane keeps, without branches, the NaN-propagating maximum over
 // its chunks, the chunk that first reached it and that chunk's raw bits; the index inside
 // the kept chunk is found once at the end.  A lane's chunks come in increasing index
@@ -463,22 +493,22 @@ __global__ __launch_bounds__(THREADS) void argmax_kernel(ArgmaxParams p) {
     if (sampled) f = gumbel_score(f, temp, ctr0 + static_cast<u32>(i), k0, k1);
     if (beats(f, i, best, bi)) { best = f; bi = i; }
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ob = __shfl_xor(best, off);
-    const int oi = __shfl_xor(bi, off);
-    if (beats(ob, oi, best, bi)) { best = ob; bi = oi; }
-  }
-  __shared__ float s_best[THREADS / 64];
-  __shared__ int s_idx[THREADS / 64];
+  // The lanes' bests as ordered keys (0: saw nothing): a plain maximum over them is the
+  // order of `beats`.  Within a wave by DPP and lane reads, across the waves through
+  // one LDS slot each, reduced by wave 0 (no LDS-routed shuffles, no serial loop).
+  const unsigned long long key = wave_max_key(bi == 0x7fffffff ? 0ull : argmax_key(best, bi));
+  __shared__ unsigned long long s_key[THREADS / 64];
   const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) { s_best[wave] = best; s_idx[wave] = bi; }
+  if ((threadIdx.x & 63) == 0) s_key[wave] = key;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < THREADS / 64; ++w)
-      if (beats(s_best[w], s_idx[w], best, bi)) { best = s_best[w]; bi = s_idx[w]; }
-    if (SPLIT) p.keys[blockIdx.x] = bi == 0x7fffffff ? 0ull : argmax_key(best, bi);
-    else p.out[blockIdx.x] = bi;
+  if (wave == 0) {
+    static_assert(THREADS / 64 <= 16, "one DPP row holds the waves' keys");
+    const int lane = threadIdx.x;
+    const unsigned long long k = row16_max_key(lane < THREADS / 64 ? s_key[lane] : 0ull);
+    if (lane == 0) {
+      if (SPLIT) p.keys[blockIdx.x] = k;
+      else p.out[blockIdx.x] = 0xffffffffu - static_cast<u32>(k & 0xffffffffu);
+    }
   }
 }
 
