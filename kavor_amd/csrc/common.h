@@ -61,6 +61,27 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// x(lane) + x(lane ^ 16) and x(lane) + x(lane ^ 32) for every lane, and the maxima, by
+// the gfx950 row / half swaps (VALU, no LDS): v_permlane16_swap_b32 (x, x) returns the
+// even rows of each row pair in both rows, then the odd rows; v_permlane32_swap_b32 (x, x)
+// returns the low half in both halves, then the high half.
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 typedef u32 u32x4_t __attribute__((ext_vector_type(4)));

@@ -287,19 +287,13 @@ __device__ __forceinline__ void emit_state(const DecodeParams& p, int b, int kvh
   const int c = lane & 15;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float mm = fmaxf(m[g], __shfl_xor(m[g], 16));
-    mm = fmaxf(mm, __shfl_xor(mm, 32));
+    const float mm = xor32_max(xor16_max(m[g]));
     const float sc = fast_exp2(m[g] - mm);
-    float ll = l[g] * sc;
-    ll += __shfl_xor(ll, 16);
-    ll += __shfl_xor(ll, 32);
+    const float ll0 = xor32_sum(xor16_sum(l[g] * sc));
     float a[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      a[j] = acc[g][j] * sc;
-      a[j] += __shfl_xor(a[j], 16);
-      a[j] += __shfl_xor(a[j], 32);
-    }
+    for (int j = 0; j < 8; ++j) a[j] = xor32_sum(xor16_sum(acc[g][j] * sc));
+    float ll = ll0;
     if (bad) ll = NAN;
     const int h = kvh * G + g;
     if (lane < 16) {
