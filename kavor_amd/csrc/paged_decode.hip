@@ -57,8 +57,8 @@ constexpr int kMinRangeTokens = 128;        // a range covers at least 128 token
 constexpr int kMinStepTokens = 16;           // smallest step (G = 8); G <= 4 steps 32 tokens
 constexpr int kMaxSeqsPerLaunch = 4096;      // size of the LDS prefix-sum table
 constexpr int kHeaderInts = 16;              // workspace header before the prefix table
-// Upper bound of the persistent grid.  Every variant holds 2 workgroups per CU on
-// MI355X (512 in all); the cap makes the workspace bound independent of the device.
+// Upper bound of the persistent grid.  The variants hold 1 or 2 workgroups per CU on
+// MI355X (at most 512 in all); the cap makes the workspace bound independent of the device.
 constexpr int kMaxDecodeGrid = 1024;
 
 struct DecodeParams {
