@@ -366,6 +366,10 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     const int row_limit = CAUSAL ? qi + diag : klen - 1;  // last key this row may see
     // smallest row_limit over this wave's rows (its first query token)
     const int wave_min_limit = CAUSAL ? q0 + (32 * wave) / G + diag : klen - 1;
+    // last key any row of this wave may see; no row of the wave is a query when its first
+    // token is past the sequence (padding rows of the last query tile)
+    const int wave_max_limit = CAUSAL ? q0 + (32 * wave + 31) / G + diag : klen - 1;
+    const bool wave_live = q0 + (32 * wave) / G < qlen;
 
     if (nkv > 0) {
       issue_k(0, s_k0);
@@ -382,6 +386,9 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         issue_k(kv0 + kKeyTile, nk);
         issue_v(kv0 + kKeyTile, nv);
       }
+      // Nothing to compute when no row of the wave sees a key of this tile: the tile would
+      // add exact zeros.  The SIMD is left to the other workgroup's wave.
+      if (!wave_live || kv0 > wave_max_limit) return;
 
       // ---- S^T = K Q^T : two 32-key blocks, lane holds keys of its own query row
       f32x16_t sacc[2];
