@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   const int member = (b % (8 * kXcdGroup)) / 8;        // which tile of the unit
   const int nseq = p.num_seqs;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases and M0 stay scalar
   const int lane = tid & 63;
   const int n = lane & 31;   // this lane's query row within the wave
   const int hf = lane >> 5;  // which half of the MFMA K-dim this lane feeds
@@ -259,6 +259,16 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   // pc ^ swz(row): K rows are swizzled by (row & 15), V rows by 4 (row & 3).  Keys past
   // the context are clamped onto its last key; their scores are masked.  Every wave of the
   // workgroup looks up the same block ids, so `bad` is uniform over the workgroup.
+  // Per-lane parts of the tile load offsets.  Lane l of an instruction covers row
+  // r0 + l/16 (r0 a multiple of 4) and physical chunk l % 16; its logical chunk is
+  // (l % 16) ^ (r & 15) for K and (l % 16) ^ 4 (r & 3) for V, where r & 15 = (r0 + l/16) & 15
+  // is the same for the 4 instructions of a wave (r0 = 4 (4 i + w)) and r & 3 = (l/16) & 3.
+  const int k_row_bytes = static_cast<int>(p.k_tok_stride) * 2;
+  const int v_row_bytes = static_cast<int>(p.v_tok_stride) * 2;
+  const int k_lane_off = (lane >> 4) * k_row_bytes;
+  const int v_lane_off = (lane >> 4) * v_row_bytes;
+  const int k_chunk_off = 16 * ((lane & 15) ^ ((4 * wave + (lane >> 4)) & 15));
+  const int v_chunk_off = 16 * ((lane & 15) ^ (4 * ((lane >> 4) & 3)));
   auto issue_k = [&](int kv0, uint16_t* dk) __attribute__((always_inline)) {
     int64_t kbase = 0;
     if (PAGED) {
@@ -279,14 +289,12 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     }
     const uint16_t* kb = p.k + kbase + static_cast<int64_t>(kvh) * p.k_head_stride;
     const BufferRsrc krs = buffer_rsrc(kb, static_cast<uint32_t>(kKeyTile * p.k_tok_stride * 2));
-    const int last = klen - 1 - kv0;
-    const int pc = lane & 15;
+    // byte offset of key min(r, last): min(r * stride, last * stride) * 2, r = r0 + lane / 16
+    const int last_off = (klen - 1 - kv0) * k_row_bytes;
 #pragma unroll
     for (int i = 0; i < kKeyTile / 4 / kPrefillWaves; ++i) {
       const int r0 = 4 * (kPrefillWaves * i + wave);
-      const int r = r0 + (lane >> 4);
-      const int key = min(r, last);
-      lds_dma16(krs, (key * static_cast<int>(p.k_tok_stride) + 8 * (pc ^ (r & 15))) * 2, &dk[r0 * kPrefillHeadDim]);
+      lds_dma16(krs, min(k_lane_off + r0 * k_row_bytes, last_off) + k_chunk_off, &dk[r0 * kPrefillHeadDim]);
     }
   };
   auto issue_v = [&](int kv0, uint16_t* dv) __attribute__((always_inline)) {
@@ -309,14 +317,11 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     }
     const uint16_t* vb = p.v + vbase + static_cast<int64_t>(kvh) * p.v_head_stride;
     const BufferRsrc vrs = buffer_rsrc(vb, static_cast<uint32_t>(kKeyTile * p.v_tok_stride * 2));
-    const int last = klen - 1 - kv0;
-    const int pc = lane & 15;
+    const int last_off = (klen - 1 - kv0) * v_row_bytes;
 #pragma unroll
     for (int i = 0; i < kKeyTile / 4 / kPrefillWaves; ++i) {
       const int r0 = 4 * (kPrefillWaves * i + wave);
-      const int r = r0 + (lane >> 4);
-      const int key = min(r, last);
-      lds_dma16(vrs, (key * static_cast<int>(p.v_tok_stride) + 8 * (pc ^ (4 * (r & 3)))) * 2, &dv[r0 * kPrefillHeadDim]);
+      lds_dma16(vrs, min(v_lane_off + r0 * v_row_bytes, last_off) + v_chunk_off, &dv[r0 * kPrefillHeadDim]);
     }
   };
 
@@ -603,6 +608,11 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
   if (!mult8(q_tok_stride) || !mult8(q_head_stride) || !mult8(k_tok_stride) || !mult8(k_head_stride) ||
       !mult8(v_tok_stride) || !mult8(v_head_stride) || (out_tok_stride & 3) || (out_head_stride & 3))
     return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: q/k/v strides must be multiples of 8, out of 4 elements");
+  // a K/V tile's 64 rows are addressed with 32-bit byte offsets
+  if (k_tok_stride <= 0 || v_tok_stride <= 0 || k_tok_stride > INT32_MAX / (2 * kKeyTile) ||
+      v_tok_stride > INT32_MAX / (2 * kKeyTile))
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: k/v token strides %lld / %lld out of range",
+                static_cast<long long>(k_tok_stride), static_cast<long long>(v_tok_stride));
 
   const int tok_per_tile = kPrefillRows / G;
   const int64_t num_tiles = (static_cast<int64_t>(max_seqlen_q) + tok_per_tile - 1) / tok_per_tile;

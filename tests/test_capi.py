@@ -158,6 +158,8 @@ def test_prefill_rejects_bad_arguments_on_host():
     assert _prefill(d=256) == _lib.KVP_EUNSUPPORTED
     assert _prefill(bt=16, bs=32, maxb=4, bts=4, nblk=8) == _lib.KVP_EINVAL  # paged, bs % 64
     assert _prefill(kts=1020) == _lib.KVP_EINVAL
+    assert _prefill(vts=1 << 24) == _lib.KVP_EINVAL              # 64 rows beyond 32-bit offsets
+    assert b"token strides" in _lib.lib().kvp_last_error()
     assert _prefill(cuq=None) == _lib.KVP_EINVAL
 
 
