@@ -708,6 +708,8 @@ PREFILL_PMC_PASSES = [
     "SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE",
     "SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_MISC "
     "SQ_INSTS_LDS SQ_CYCLES SQ_WAIT_INST_LDS GRBM_GUI_ACTIVE",
+    "SQ_INSTS_LDS_LOAD_BANDWIDTH SQ_LDS_IDX_ACTIVE TA_TA_BUSY TA_ADDR_STALLED_BY_TC_CYCLES TD_TD_BUSY "
+    "TD_TC_STALL GRBM_GUI_ACTIVE",
 ]
 PREFILL_PMC_CMDS = [
     "cd /tmp && export TMPDIR=/tmp",
@@ -715,13 +717,15 @@ PREFILL_PMC_CMDS = [
     "python $R/bench.py --profile-prefill",
     "rocprofv3 --pmc " + PREFILL_PMC_PASSES[1] + " --output-format csv -d $OUT/ppmc_b -o run -- "
     "python $R/bench.py --profile-prefill",
-    "python $R/bench.py --summarize-prefill-pmc $OUT/ppmc_a $OUT/ppmc_b",
+    "rocprofv3 --pmc " + PREFILL_PMC_PASSES[2] + " --output-format csv -d $OUT/ppmc_c -o run -- "
+    "python $R/bench.py --profile-prefill",
+    "python $R/bench.py --summarize-prefill-pmc $OUT/ppmc_a $OUT/ppmc_b $OUT/ppmc_c",
 ]
 
 
-def summarize_prefill_pmc(dir_a: str, dir_b: str) -> int:
+def summarize_prefill_pmc(dir_a: str, dir_b: str, dir_c: str) -> int:
     """profiles/varlen_prefill_prefix_32seq_pmc.md: where the prefill kernel's cycles go,
-    from two rocprofv3 --pmc passes over --profile-prefill (medians over the dispatches
+    from three rocprofv3 --pmc passes over --profile-prefill (medians over the dispatches
     after the first third).  Counters are summed over the device; GRBM_GUI_ACTIVE counts
     once per XCD, so one XCD's busy cycles are its sum divided by the XCD count."""
     import csv
@@ -730,7 +734,7 @@ def summarize_prefill_pmc(dir_a: str, dir_b: str) -> int:
     name = "void kvp::varlen_prefill_kernel<2, true, true>"
     vals = defaultdict(lambda: defaultdict(float))
     agent = {}
-    for d in (dir_a, dir_b):
+    for d in (dir_a, dir_b, dir_c):
         for r in csv.DictReader(open(Path(d) / "run_counter_collection.csv")):
             if r["Kernel_Name"].startswith(name):
                 vals[(d, int(r["Dispatch_Id"]))][r["Counter_Name"]] += float(r["Counter_Value"])
@@ -796,6 +800,13 @@ def summarize_prefill_pmc(dir_a: str, dir_b: str) -> int:
         f"| VALU / LDS issue | {100 * med('SQ_ACTIVE_INST_VALU')[0] / wave_cycles:.1f}% / "
         f"{100 * med('SQ_ACTIVE_INST_LDS')[0] / wave_cycles:.1f}% of wave cycles | SQ_ACTIVE_INST_VALU, "
         "SQ_ACTIVE_INST_LDS / SQ_WAVE_CYCLES |",
+        f"| LDS reads | {med('SQ_INSTS_LDS_LOAD_BANDWIDTH')[0] * 64 / 1e9:.2f} GB per call = "
+        f"{med('SQ_INSTS_LDS_LOAD_BANDWIDTH')[0] * 64 / (xcd_cycles * cus):.1f} B per cycle per CU "
+        "(MFMA operands; the tiles' direct-to-LDS writes come on top) | SQ_INSTS_LDS_LOAD_BANDWIDTH x 64 B |",
+        f"| texture address / data units busy | {100 * med('TA_TA_BUSY')[0] / (xcd_cycles * cus):.1f}% / "
+        f"{100 * med('TD_TD_BUSY')[0] / (xcd_cycles * cus):.1f}% of cycles per CU (TD waiting on the "
+        f"L1: {100 * med('TD_TC_STALL')[0] / (xcd_cycles * cus):.1f}%) | TA_TA_BUSY, TD_TD_BUSY, TD_TC_STALL "
+        "/ (cycles x CUs) |",
     ]
     out = ROOT / "profiles" / "varlen_prefill_prefix_32seq_pmc.md"
     out.write_text("\n".join(lines) + "\n")
@@ -1170,8 +1181,8 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="only the prefix-cached prefill launches (30), for rocprofv3 --pmc passes")
-    ap.add_argument("--summarize-prefill-pmc", nargs=2, metavar=("PASS_A_DIR", "PASS_B_DIR"),
-                    help="write profiles/varlen_prefill_prefix_32seq_pmc.md from the two --pmc passes")
+    ap.add_argument("--summarize-prefill-pmc", nargs=3, metavar=("PASS_A_DIR", "PASS_B_DIR", "PASS_C_DIR"),
+                    help="write profiles/varlen_prefill_prefix_32seq_pmc.md from the three --pmc passes")
     ap.add_argument("--summarize-e2e", nargs="+", metavar="TRACE_DIR [CALLER]",
                     help="write profiles/e2e_qwen3_0.6b.md from rocprofv3 --stats over --e2e-only")
     args = ap.parse_args()
