@@ -26,10 +26,13 @@
 //   Work order: every workgroup ranks the units of work (a pair of neighbouring query
 //   tiles of one sequence and kv head) by cost and takes the one of its own rank, so
 //   the most expensive units start first and the cheap ones fill in behind them; the
-//   two tiles of a unit run on one XCD.
+//   two tiles of a unit run on one XCD.  Dense prefill runs persistent workgroups that
+//   take every grid-th rank, so the many short units of a batch without prefixes do not
+//   each pay a workgroup's start-up.
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "common.h"
 
@@ -46,6 +49,9 @@ constexpr int kXcdGroup = 2;  // neighbouring query tiles of one (sequence, kv h
 // launches.
 constexpr int kMaxPrefillSeqs = 2048;
 static_assert(kKeyTile * kPrefillHeadDim * 2 >= kMaxPrefillSeqs * 8, "lengths must fit one tile buffer");
+// Dense prefill runs persistent workgroups, which keep the lengths in LDS of their own
+// across units: up to 1024 sequences per launch (8 KiB; 72 KiB per workgroup in all).
+constexpr int kMaxDenseSeqs = 1024;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -118,9 +124,14 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   // (sequence, kv head, tile) order, and 0.457 -> 0.437 ms for the global cost order
   // against "last tiles first".  The rank is found by a binary search over cost levels
   // on closed-form unit counts per sequence (no sort, no workspace).
-  const int b = blockIdx.x;
-  const int m0 = (b / (8 * kXcdGroup)) * 8 + (b % 8);  // this workgroup pair's rank
-  const int member = (b % (8 * kXcdGroup)) / 8;        // which tile of the unit
+  int b = blockIdx.x;
+  int m0 = (b / (8 * kXcdGroup)) * 8 + (b % 8);  // this workgroup pair's rank
+  int member = (b % (8 * kXcdGroup)) / 8;        // which tile of the unit
+  // Dense: persistent workgroups.  Workgroup b takes the units of ranks m0(b),
+  // m0(b + grid), ... (the grid is a multiple of 16, so b + k grid keeps b's XCD and pair
+  // member).  Paged: one unit per workgroup, placed by the hardware's dispatch, which
+  // balances the very unequal units of prefix-cached batches better than a static deal.
+  constexpr bool PERSIST = !PAGED;
   const int nseq = p.num_seqs;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases and M0 stay scalar
@@ -133,12 +144,13 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   __shared__ __attribute__((aligned(16))) uint16_t s_k0[kKeyTile * kPrefillHeadDim];
   __shared__ __attribute__((aligned(16))) uint16_t s_k1[kKeyTile * kPrefillHeadDim];
   __shared__ __attribute__((aligned(16))) uint16_t s_v0[kKeyTile * kPrefillHeadDim];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v1[kKeyTile * kPrefillHeadDim];
+  // (dense: the lengths, kept across units, follow the last tile buffer)
+  __shared__ __attribute__((aligned(16))) uint16_t s_v1[kKeyTile * kPrefillHeadDim + (PERSIST ? 4 * kMaxDenseSeqs : 0)];
 
   // Before the first K/V tile is staged, the K buffers hold every sequence's
   // (query length, key length) and the V buffers its (query start, key start).
-  int2* s_len = reinterpret_cast<int2*>(&s_k0[0]);
-  int2* s_start = reinterpret_cast<int2*>(&s_v0[0]);
+  int2* s_len = reinterpret_cast<int2*>(PERSIST ? &s_v1[kKeyTile * kPrefillHeadDim] : &s_k0[0]);
+  int2* s_start = reinterpret_cast<int2*>(&s_v0[0]);  // paged only
   const int J = p.pair_slots;  // tile pairs per (sequence, kv head) the grid covers
 
   // Units of sequence (ql, kl) whose first tile needs at least L key tiles.  Tile i of
@@ -178,14 +190,16 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   for (int i = tid; i < nseq; i += kPrefillThreads) {
     const int q0s = p.cu_q[i], q1s = p.cu_q[i + 1], k0s = p.cu_k[i], k1s = p.cu_k[i + 1];
     s_len[i] = make_int2(q1s - q0s, k1s - k0s);
-    s_start[i] = make_int2(q0s, k0s);
+    if (!PERSIST) s_start[i] = make_int2(q0s, k0s);
   }
   __syncthreads();
+  const int total_units = count_ge(0);
 
+  for (;;) {
   // Rank r in the order of decreasing cost (ties: sequence, kv head, unit).  Every wave
   // computes the same answer.
   const int r = m0;
-  if (r >= count_ge(0)) return;  // uniform; no barrier follows
+  if (r >= total_units) break;  // uniform; no barrier follows
   int kmax = 0;
   for (int i = lane; i < nseq; i += 64) kmax = max(kmax, s_len[i].y);
   int lo = 0, hi = (wave_max(kmax) + kKeyTile - 1) / kKeyTile + 1, c_hi = 0;
@@ -223,7 +237,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     }
     rr -= tot;
   }
-  if (s < 0) return;  // unreachable while the counts agree (uniform)
+  if (s < 0) break;  // unreachable while the counts agree (uniform)
   // Every lane holds the same values: readfirstlane keeps them (and the addresses
   // derived from them) in scalar registers.
   s = __builtin_amdgcn_readfirstlane(s);
@@ -232,13 +246,13 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   const int kvh = rr / per_head;
   const int jj = __builtin_amdgcn_readfirstlane(skip) + rr % per_head;
   const int2 ls = s_len[s];
-  const int2 st = s_start[s];
+  const int2 st = PERSIST ? make_int2(p.cu_q[s], p.cu_k[s]) : s_start[s];
   const int q_start = __builtin_amdgcn_readfirstlane(st.x);
   const int qlen = __builtin_amdgcn_readfirstlane(ls.x);
   const int k_start = __builtin_amdgcn_readfirstlane(st.y);
   const int klen = __builtin_amdgcn_readfirstlane(ls.y);
   const int diag = klen - qlen;  // bottom-right causal offset
-  __syncthreads();  // every wave has read the lengths: the buffers may be staged
+  if (!PERSIST) __syncthreads();  // every wave has read the lengths: the buffers may be staged
 
   bool bad = false;
   if (PAGED && klen > p.max_blocks * p.block_size) bad = true;
@@ -543,17 +557,52 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         }
     }
   }
+  if (!PERSIST) break;
+  b += gridDim.x;
+  m0 = (b / (8 * kXcdGroup)) * 8 + (b % 8);
+  member = (b % (8 * kXcdGroup)) / 8;
+  }  // next unit
+}
+
+// Workgroups of one kernel variant resident on the current device (cached per variant and
+// device), rounded down to whole groups of 16 (one pair on each XCD).
+template <int G, bool PAGED, bool CAUSAL>
+static int64_t prefill_resident() {
+  static std::atomic<int64_t> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int64_t v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int per_cu = 0, cus = 0;
+  bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, varlen_prefill_kernel<G, PAGED, CAUSAL>,
+                                                         kPrefillThreads, 0) == hipSuccess && per_cu >= 1;
+  if (!ok) per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) {
+    cus = 16;
+    ok = false;
+  }
+  v = std::max<int64_t>(16, static_cast<int64_t>(per_cu) * cus / 16 * 16);
+  if (ok) cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// `total` is the unit-pair slot count rounded up to a multiple of 16: one workgroup per
+// slot (paged), or the resident count of persistent workgroups if smaller (dense).
+template <int G, bool PAGED, bool CAUSAL>
+static void launch_variant(int64_t total, hipStream_t s, const PrefillParams& p) {
+  const int64_t grid = PAGED ? total : std::min<int64_t>(total, prefill_resident<G, PAGED, CAUSAL>());
+  hipLaunchKernelGGL((varlen_prefill_kernel<G, PAGED, CAUSAL>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kPrefillThreads), 0, s, p);
 }
 
 template <int G>
-static void launch_prefill(bool paged, bool causal, dim3 grid, hipStream_t s, const PrefillParams& p) {
-  const dim3 block(kPrefillThreads);
+static void launch_prefill(bool paged, bool causal, int64_t total, hipStream_t s, const PrefillParams& p) {
   if (paged) {
-    if (causal) hipLaunchKernelGGL((varlen_prefill_kernel<G, true, true>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((varlen_prefill_kernel<G, true, false>), grid, block, 0, s, p);
+    if (causal) launch_variant<G, true, true>(total, s, p);
+    else launch_variant<G, true, false>(total, s, p);
   } else {
-    if (causal) hipLaunchKernelGGL((varlen_prefill_kernel<G, false, true>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((varlen_prefill_kernel<G, false, false>), grid, block, 0, s, p);
+    if (causal) launch_variant<G, false, true>(total, s, p);
+    else launch_variant<G, false, false>(total, s, p);
   }
 }
 
@@ -648,19 +697,19 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
   const bool c = causal != 0;
   // cu_seqlens hold absolute offsets, so a launch over sequences [s0, s0 + n) reads
   // the same q/k/out rows through the offset pointers.
-  for (int s0 = 0; s0 < num_seqs; s0 += kMaxPrefillSeqs) {
-    const int n = std::min(kMaxPrefillSeqs, num_seqs - s0);
+  const int chunk = paged ? kMaxPrefillSeqs : kMaxDenseSeqs;
+  for (int s0 = 0; s0 < num_seqs; s0 += chunk) {
+    const int n = std::min(chunk, num_seqs - s0);
     p.cu_q = cu_seqlens_q + s0;
     p.cu_k = cu_seqlens_k + s0;
     p.block_tables = paged ? block_tables + s0 * block_table_stride : nullptr;
     p.num_seqs = n;
-    const int64_t total = pair_slots * num_kv_heads * n * kXcdGroup;
-    const dim3 grid(static_cast<unsigned>((total + kRound - 1) / kRound * kRound));
+    const int64_t total = (pair_slots * num_kv_heads * n * kXcdGroup + kRound - 1) / kRound * kRound;
     switch (G) {
-      case 1: launch_prefill<1>(paged, c, grid, s, p); break;
-      case 2: launch_prefill<2>(paged, c, grid, s, p); break;
-      case 4: launch_prefill<4>(paged, c, grid, s, p); break;
-      default: launch_prefill<8>(paged, c, grid, s, p); break;
+      case 1: launch_prefill<1>(paged, c, total, s, p); break;
+      case 2: launch_prefill<2>(paged, c, total, s, p); break;
+      case 4: launch_prefill<4>(paged, c, total, s, p); break;
+      default: launch_prefill<8>(paged, c, total, s, p); break;
     }
     const int rc = launch_status("kvp_varlen_prefill_bf16");
     if (rc != KVP_OK) return rc;

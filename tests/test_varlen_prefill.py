@@ -238,6 +238,24 @@ def test_many_sequences_and_query_tile_pairs(cuda_device):
     torch.testing.assert_close(out.cpu().float(), want, **TOL)
 
 
+def test_dense_persistent_workgroups_take_many_units(cuda_device):
+    """Dense prefill runs persistent workgroups.  320 sequences of 1-400 tokens with an
+    understated max_seqlen_q (so a unit spans several tile pairs) give each workgroup
+    many units of unequal cost.  Every row equals the paged instance's (one unit per
+    workgroup) bit for bit, and the oracle within tolerance."""
+    g = gen(256)
+    qlens = [int(x) for x in torch.randint(1, 401, (320,), generator=g)]
+    q, kc, vc, bt, cq, ck = _paged_case(257, qlens, [0] * len(qlens), 16, 8, 64)
+    kd = torch.cat([ref._gather_tokens(kc, bt[s], qlens[s]) for s in range(len(qlens))])
+    vd = torch.cat([ref._gather_tokens(vc, bt[s], qlens[s]) for s in range(len(qlens))])
+    d = cuda_device
+    dense = _prefill(q.to(d), kd.to(d), vd.to(d), cq.to(d), cq.to(d), 100)
+    paged = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), 100, bt=bt.to(d))
+    torch.cuda.synchronize()
+    assert bits_equal(dense.cpu(), paged.cpu())
+    torch.testing.assert_close(dense.cpu().float(), ref.varlen_prefill(q, kd, vd, cq, cq, SCALE), **TOL)
+
+
 def test_paged_relocated_pages_are_bitwise_identical(cuda_device):
     """Prefix-cached prefill over pages moved to other physical blocks (tables renumbered
     to match) gives identical bits."""
@@ -252,9 +270,9 @@ def test_paged_relocated_pages_are_bitwise_identical(cuda_device):
 
 @pytest.mark.parametrize("paged", [True, False])
 def test_more_sequences_than_one_launch(cuda_device, paged):
-    """4100 sequences run as three launches (2048 + 2048 + 4): the later ones read their
-    cu_seqlens and block-table rows through offset pointers and write the same absolute
-    rows."""
+    """4100 sequences run as several launches (paged: 2048 + 2048 + 4; dense: 4 x 1024 +
+    4): the later ones read their cu_seqlens and block-table rows through offset pointers
+    and write the same absolute rows."""
     g = gen(260 + paged)
     nseq, bs, nb = 4100, 64, 64
     qlens = [int(x) for x in torch.randint(1, 4, (nseq,), generator=g)]
