@@ -55,6 +55,7 @@ constexpr int kDecodeWaves = 4;  // kv heads per workgroup
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kMinRangeTokens = 128;        // a range covers at least 128 tokens
 constexpr int kMinStepTokens = 16;           // smallest step (G = 8); G <= 4 steps 32 tokens
+constexpr int kG5Step = 16;                  // G = 5 (Qwen3-14B: 40 q heads over 8 kv heads)
 constexpr int kMaxSeqsPerLaunch = 4096;      // size of the LDS prefix-sum table
 constexpr int kHeaderInts = 16;              // workspace header before the prefix table
 // Upper bound of the persistent grid.  The variants hold 1 or 2 workgroups per CU on
@@ -790,6 +791,7 @@ static int64_t decode_ranges_for(int G, int num_kv_heads, int64_t max_tokens) {
     case 1: return decode_ranges<1, 32, FUSED>(num_kv_heads, max_tokens);
     case 2: return decode_ranges<2, 32, FUSED>(num_kv_heads, max_tokens);
     case 4: return decode_ranges<4, 32, FUSED>(num_kv_heads, max_tokens);
+    case 5: return decode_ranges<5, kG5Step, FUSED>(num_kv_heads, max_tokens);
     default: return decode_ranges<8, kMinStepTokens, FUSED>(num_kv_heads, max_tokens);
   }
 }
@@ -829,8 +831,8 @@ static int check_decode_args(const char* fn, const DecodeArgs& a) {
     return fail(KVP_EINVAL, "%s: num_q_heads=%d not a multiple of num_kv_heads=%d", fn, a.num_q_heads,
                 a.num_kv_heads);
   const int G = a.num_q_heads / a.num_kv_heads;
-  if (G != 1 && G != 2 && G != 4 && G != 8)
-    return fail(KVP_EUNSUPPORTED, "%s: GQA ratio %d (supported: 1, 2, 4, 8)", fn, G);
+  if (G != 1 && G != 2 && G != 4 && G != 5 && G != 8)
+    return fail(KVP_EUNSUPPORTED, "%s: GQA ratio %d (supported: 1, 2, 4, 5, 8)", fn, G);
   if (a.block_size <= 0 || a.block_size % 64 != 0)
     return fail(KVP_EINVAL, "%s: block_size=%d must be a positive multiple of 64", fn, a.block_size);
   if (a.max_blocks_per_seq <= 0 || a.num_cache_blocks <= 0)
@@ -898,6 +900,7 @@ static int enqueue_decode(const char* fn, const DecodeArgs& a, int64_t ranges, c
       case 1: launch_decode<1, 32, FUSED>(p, ranges, s); break;
       case 2: launch_decode<2, 32, FUSED>(p, ranges, s); break;
       case 4: launch_decode<4, 32, FUSED>(p, ranges, s); break;
+      case 5: launch_decode<5, kG5Step, FUSED>(p, ranges, s); break;
       default: launch_decode<8, kMinStepTokens, FUSED>(p, ranges, s); break;
     }
     const int rc = launch_status(fn);

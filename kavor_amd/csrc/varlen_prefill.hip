@@ -361,7 +361,8 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     const int tq = rho / G;
     const int g = rho - tq * G;
     const int qi = q0 + tq;  // query index within the sequence
-    const bool row_valid = qi < qlen;
+    // rows past the tile's TOK whole tokens (G = 5: 125 of 128) are padding
+    const bool row_valid = tq < TOK && qi < qlen;
 
     uint4 qreg[D / 16];
     {
@@ -634,8 +635,8 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
     return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: num_q_heads=%d not a multiple of num_kv_heads=%d",
                 num_q_heads, num_kv_heads);
   const int G = num_q_heads / num_kv_heads;
-  if (G != 1 && G != 2 && G != 4 && G != 8)
-    return fail(KVP_EUNSUPPORTED, "kvp_varlen_prefill_bf16: GQA ratio %d (supported: 1, 2, 4, 8)", G);
+  if (G != 1 && G != 2 && G != 4 && G != 5 && G != 8)
+    return fail(KVP_EUNSUPPORTED, "kvp_varlen_prefill_bf16: GQA ratio %d (supported: 1, 2, 4, 5, 8)", G);
   const bool paged = block_tables != nullptr;
   if (paged) {
     if (block_size <= 0 || block_size % kKeyTile != 0)
@@ -709,6 +710,7 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
       case 1: launch_prefill<1>(paged, c, total, s, p); break;
       case 2: launch_prefill<2>(paged, c, total, s, p); break;
       case 4: launch_prefill<4>(paged, c, total, s, p); break;
+      case 5: launch_prefill<5>(paged, c, total, s, p); break;
       default: launch_prefill<8>(paged, c, total, s, p); break;
     }
     const int rc = launch_status("kvp_varlen_prefill_bf16");

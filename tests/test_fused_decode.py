@@ -58,7 +58,7 @@ def _fused(d, hq, hkv, bs):
                               d["slots"], d["ctx"], d["bt"], D ** -0.5)
 
 
-@pytest.mark.parametrize("G,hkv,bs", [(1, 2, 64), (2, 8, 256), (4, 8, 256), (8, 2, 128)])
+@pytest.mark.parametrize("G,hkv,bs", [(1, 2, 64), (2, 8, 256), (4, 8, 256), (5, 8, 256), (8, 2, 128)])
 def test_fused_decode_equals_separate_launches(cuda_device, G, hkv, bs):
     hq = G * hkv
     ctxs = [1, 2, bs, bs + 1, 3 * bs - 1, 1500, 4000, 777]

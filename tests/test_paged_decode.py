@@ -44,7 +44,7 @@ def _check(dev, q, kc, vc, bt, ctx, tol=TOL):
     return out
 
 
-@pytest.mark.parametrize("G", [1, 2, 4, 8])
+@pytest.mark.parametrize("G", [1, 2, 4, 5, 8])
 @pytest.mark.parametrize("bs,layout", [(256, "interleaved"), (64, "contiguous"), (128, "interleaved")])
 def test_decode_matches_oracle(cuda_device, G, bs, layout):
     hkv = 2
@@ -293,7 +293,7 @@ def test_decode_back_to_back_shapes_share_the_workspace(cuda_device):
     The cases cover every GQA ratio and sequences cut into many parts."""
     d = cuda_device
     cases = [(40, 8, 1, 64, 4000, 9000), (3, 64, 8, 256, 20000, 30000), (64, 16, 8, 256, 1, 2048),
-             (7, 8, 2, 128, 900, 5000), (5, 16, 4, 64, 3000, 7000)]
+             (7, 8, 2, 128, 900, 5000), (5, 16, 4, 64, 3000, 7000), (24, 40, 8, 256, 1, 4000)]
     for i, (B, hq, hkv, bs, lo, hi) in enumerate(cases):
         q, kc, vc, bt, ctx = _case(40 + i, B=B, hq=hq, hkv=hkv, bs=bs, lo=lo, hi=hi)
         _check(d, q, kc, vc, bt, ctx)

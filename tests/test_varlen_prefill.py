@@ -40,7 +40,7 @@ def _dense_case(seed, qlens, hq, hkv, qkv_view=True):
     return q, k, v
 
 
-@pytest.mark.parametrize("G", [1, 2, 4, 8])
+@pytest.mark.parametrize("G", [1, 2, 4, 5, 8])
 def test_dense_causal_matches_oracle(cuda_device, G):
     hkv = 2
     qlens = [1, 17, 64, 65, 200, 333]
@@ -78,7 +78,7 @@ def _paged_case(seed, qlens, prefix, hq, hkv, bs, layout="interleaved", nb=None)
 
 
 @pytest.mark.parametrize("bs,layout", [(256, "interleaved"), (64, "contiguous")])
-@pytest.mark.parametrize("G", [2, 4])
+@pytest.mark.parametrize("G", [2, 4, 5])
 def test_paged_prefix_matches_oracle(cuda_device, bs, layout, G):
     """Prefix-cached prefill over the pages: block-aligned prefixes (prefix-cache hits),
     unaligned ones (chunked prefill, scheduler.py:124) and empty ones in one batch."""
