@@ -55,7 +55,7 @@ constexpr int kDecodeWaves = 4;  // kv heads per workgroup
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kMinRangeTokens = 128;        // a range covers at least 128 tokens
 constexpr int kMinStepTokens = 16;           // smallest step (G = 8); G <= 4 steps 32 tokens
-constexpr int kG5Step = 16;                  // G = 5 (Qwen3-14B: 40 q heads over 8 kv heads)
+constexpr int kG5Step = 32;                  // G = 5 (Qwen3-14B: 40 q heads over 8 kv heads)
 constexpr int kMaxSeqsPerLaunch = 4096;      // size of the LDS prefix-sum table
 constexpr int kHeaderInts = 16;              // workspace header before the prefix table
 // Upper bound of the persistent grid.  The variants hold 1 or 2 workgroups per CU on
