@@ -254,6 +254,31 @@ def test_separate_decode_launches_match_reference(cuda_device):
 
 
 
+@pytest.mark.parametrize("caller", ["fused", "dropin"])
+def test_gqa_ratio_5_engine_matches_reference(cuda_device, caller):
+    """Qwen3-14B's head ratio (40 query heads over 8 kv heads) at a small size, 10 over 2:
+    prefill (tiles of 25 whole tokens), prefix hits, graph-replayed and eager decode
+    through both callers, every token checked."""
+    spec = Qwen3Spec(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                     num_attention_heads=10, num_key_value_heads=2, head_dim=128,
+                     max_position_embeddings=4096, eos_token_id=1)
+    llm = LLM(spec, kvcache_block_size=64, max_model_len=1024, num_kvcache_blocks=128,
+              max_num_seqs=8, max_num_batched_tokens=1024, attention_caller=caller, seed=0)
+    try:
+        assert llm.model_runner.graphs
+        base = _prompts(21, [130], spec.vocab_size)[0]
+        prompts = [base, _prompts(22, [1], spec.vocab_size)[0], _prompts(23, [77], spec.vocab_size)[0]]
+        sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True) for m in (24, 10, 31)]
+        outs = llm.generate(prompts, sps)
+        again = [base + [5, 6, 7]]
+        outs2 = llm.generate(again, SamplingParams(temperature=0.0, max_tokens=15, ignore_eos=True))
+        assert llm.scheduler.block_manager.prefix_cache_hit_tokens >= 128
+        for p, o in zip(prompts + again, outs + outs2):
+            check_greedy_tokens(llm.model_runner.model, p, o["token_ids"], TOL)
+    finally:
+        llm.exit()
+
+
 def test_copy_blocks_on_device_pages_feed_the_decode(cuda_device):
     """copy_blocks (cache_pool.py:142-149) on a device pool: the copied pages equal their
     sources byte for byte in every layer, the other pages keep their bytes, and paged
