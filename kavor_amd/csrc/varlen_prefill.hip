@@ -139,8 +139,8 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   const int n = lane & 31;   // this lane's query row within the wave
   const int hf = lane >> 5;  // which half of the MFMA K-dim this lane feeds
 
-  // Two buffers of the K and V tiles (row-major, padded rows): tile i+1 is written while
-  // other waves may still read tile i.
+  // Two buffers of the K and V tiles (row-major, unpadded, 16-byte chunks XOR-swizzled
+  // per row): tile i+1 is written while other waves may still read tile i.
   __shared__ __attribute__((aligned(16))) uint16_t s_k0[kKeyTile * kPrefillHeadDim];
   __shared__ __attribute__((aligned(16))) uint16_t s_k1[kKeyTile * kPrefillHeadDim];
   __shared__ __attribute__((aligned(16))) uint16_t s_v0[kKeyTile * kPrefillHeadDim];
