@@ -126,3 +126,31 @@ def test_fused_decode_replays_in_a_graph(cuda_device):
         torch.cuda.synchronize()
         assert torch.equal(out.cpu().view(torch.int16), eager.cpu().view(torch.int16))
         assert torch.equal(d["pool"].cpu(), d2["pool"].cpu())
+
+
+@pytest.mark.parametrize("seed", range(int(__import__("os").environ.get("KVP_RANDOM_CASES", "12"))))
+def test_fused_decode_random_shapes(cuda_device, seed):
+    """Seeded random batches (GQA 1, 2, 4, 5 or 8, block sizes 64-512, contexts from one
+    token to several pages, padding rows): the pools equal the separate launches' byte
+    for byte and the output matches the oracle."""
+    g = gen(7000 + seed)
+    pick = lambda xs: xs[int(torch.randint(0, len(xs), (1,), generator=g))]
+    G, bs = pick([1, 2, 4, 5, 8]), pick([64, 128, 256, 512])
+    hkv = pick([1, 2, 4, 8]) if G != 8 else pick([1, 2])
+    hq = G * hkv
+    B = int(torch.randint(1, 40, (1,), generator=g))
+    hi = int(torch.randint(1, 5000, (1,), generator=g))
+    ctxs = [int(x) for x in torch.randint(1, hi + 1, (B,), generator=g)]
+    pad = int(torch.randint(0, 3, (1,), generator=g))
+    print(f"fused decode seed={seed} G={G} hkv={hkv} bs={bs} B={B} pad={pad} ctx<= {hi}", flush=True)
+    host, d1 = _case(cuda_device, 7100 + seed, hq, hkv, bs, ctxs, pad=pad)
+    d2 = {k: v.clone() for k, v in d1.items()}
+    o_sep = _separate(d1, hq, hkv, bs)
+    o_fused = _fused(d2, hq, hkv, bs)
+    torch.cuda.synchronize()
+    assert torch.equal(d1["pool"].cpu(), d2["pool"].cpu())
+    kc, vc = ref.page_views(d2["pool"].cpu(), bs, hkv, D)
+    wq, _, _ = lref.qk_norm_rope(host["qkv"], host["pos"], host["table"], host["qw"], host["kw"], EPS, hq, hkv)
+    want = ref.paged_decode(wq, kc, vc, host["bt"], host["ctx"], D ** -0.5)
+    torch.testing.assert_close(o_fused.cpu().float(), want, **TOL)
+    torch.testing.assert_close(o_fused.cpu().float(), o_sep.cpu().float(), **TOL)
