@@ -84,6 +84,21 @@ __device__ __forceinline__ float xor32_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active): DPP right shifts by
+// 1, 2, 4 and 8 inside each 16-lane row (lanes shifted in from outside the row read 0),
+// then the totals of the rows below, read with readlane.  No LDS round trips.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15);
+  const int r1 = r0 + __builtin_amdgcn_readlane(x, 31);
+  const int r2 = r1 + __builtin_amdgcn_readlane(x, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return x + (row == 0 ? 0 : (row == 1 ? r0 : (row == 2 ? r1 : r2)));
+}
+
 typedef u32 u32x4_t __attribute__((ext_vector_type(4)));
 
 // 16-byte load / store with the nontemporal hint, for data touched exactly once (KV rows

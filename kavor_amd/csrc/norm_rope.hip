@@ -87,10 +87,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(NormParams p) {
     }
   }
   ss = row16_sum(ss);
-  if (LANES == 64) {
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-  }
+  if (LANES == 64) ss = xor32_sum(xor16_sum(ss));
   const float rstd = rsqrtf(ss / static_cast<float>(p.cols) + p.eps);
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {

@@ -119,7 +119,7 @@ __device__ __forceinline__ int seq_steps(int ctx, const DecodeParams& p) {
 
 // s_cum[b] = steps of sequences 0..b-1 (b = 0..num_seqs), built by the whole workgroup:
 // each thread sums a contiguous run of sequences, then the 256 run totals are scanned
-// with shuffles within each wave and the 4 wave totals through LDS (one barrier; a
+// with DPP within each wave and the 4 wave totals through LDS (one barrier; a
 // Hillis-Steele scan over LDS took 16: 15.0 -> 14.65 us per call for 4 sequences).
 __device__ void build_step_prefix(const DecodeParams& p, int* s_cum, int* s_part) {
   const int tid = threadIdx.x;
@@ -145,15 +145,10 @@ __device__ void build_step_prefix(const DecodeParams& p, int* s_cum, int* s_part
       *reinterpret_cast<uint4*>(p.out + b * p.o_seq_stride + h * p.o_head_stride + d) = f;
     }
   }
-  // Inclusive scan of the run totals within each wave (shuffles), then across the 4
-  // waves through LDS: one barrier.
+  // Inclusive scan of the run totals within each wave (DPP and lane reads), then across
+  // the 4 waves through LDS: one barrier.
   const int lane = tid & 63, wave = tid >> 6;
-  int incl = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int v = __shfl_up(incl, off);
-    if (lane >= off) incl += v;
-  }
+  const int incl = wave_incl_scan(local);
   if (lane == 63) s_part[wave] = incl;
   __syncthreads();
   int before = 0;
