@@ -192,6 +192,9 @@ def bench_decode(dev, steps, warmup, shape):
     def step():
         paged_decode(inp["q"], inp["kc"], inp["vc"], inp["ctx"], inp["bt"], SCALE, out=out)
 
+    # settle the clocks on wall time before the timed launches (a few warm-up calls of a
+    # 0.17 ms kernel leave the part below its sustained clock)
+    warm_for(step, 0.5)
     ms = time_launches(step, steps, warmup)
     nbytes = decode_bytes(inp["ctx_host"].tolist(), inp["hq"], inp["hkv"], D, BS)
     return inp, dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
@@ -265,7 +268,9 @@ def bench_append(dev, steps, warmup):
     with torch.cuda.graph(graph):
         for k, v, s in sets:
             store_kvcache(k, v, kc, vc, s)
-    replays = max(2, (steps if steps < 16 else max(steps, 48)) // len(sets))
+    # at least 10 replays (240 appends) are timed, after the clocks have settled
+    replays = max(10, steps // len(sets))
+    warm_for(graph.replay, 0.3)
     ms = time_launches(graph.replay, replays, max(1, warmup // len(sets))) / len(sets)
     nbytes = append_bytes(sets[0][2].cpu().tolist(), hkv, D)
     # The engine's layout: one 1 MiB page per block holding K then V (block stride
@@ -281,6 +286,7 @@ def bench_append(dev, steps, warmup):
     with torch.cuda.graph(pgraph):
         for k, v, s in sets:
             store_kvcache(k, v, kp, vp, s)
+    warm_for(pgraph.replay, 0.3)
     paged_ms = time_launches(pgraph.replay, replays, max(1, warmup // len(sets))) / len(sets)
     del pgraph, pool, kp, vp
     # The same bytes moved by a plain device copy (torch's copy kernel), timed the same
@@ -296,6 +302,7 @@ def bench_append(dev, steps, warmup):
     with torch.cuda.graph(cgraph):
         for x, y in zip(srcs, dsts):
             y.copy_(x)
+    warm_for(cgraph.replay, 0.3)
     copy_ms = time_launches(cgraph.replay, replays, max(1, warmup // len(sets))) / len(srcs)
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6, copy_ms=copy_ms, paged_ms=paged_ms)
 
@@ -382,6 +389,7 @@ def bench_layers(dev, steps, warmup):
     algo = layer_algo_bytes(inp)
     res = {}
     for name, fn in layer_launchers(inp).items():
+        warm_for(fn, 0.3)  # settled clocks before each kernel's timed launches
         # the 16-row argmax (about 6 us) is timed as graph replays, as the engine runs it
         ms = (time_graph if name == "argmax_16rows" else time_launches)(fn, steps, warmup)
         res[name] = dict(us=round(ms * 1e3, 2), gbs=round(algo[name] / ms / 1e6, 1),

@@ -155,11 +155,17 @@ int kvp_paged_decode_fused_bf16(const void* qkv, int64_t qkv_tok_stride,
  * the reference: it is for callers that cannot allocate device memory (code under
  * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, semantics and results as kvp_paged_decode_bf16 (bit for bit).  A batch
- * whose partial states do not fit (about (512 + num_seqs) * num_q_heads * 520 bytes on
+ * whose partial states do not fit (about (R + num_seqs) * num_q_heads * 520 bytes, where
+ * R <= 1024 is the launch's range count: the resident workgroups divided by
+ * ceil(num_kv_heads / 4), so 512 with 8 kv heads and up to 1024 with 4 or fewer on
  * MI355X; Qwen3-0.6B at 512 sequences takes 8.5 MB) returns KVP_EWORKSPACE before any
  * launch.  Every call on one GPU shares that GPU's array, so calls that overlap on one
  * GPU (different streams or threads without ordering) race; calls ordered on one
- * stream do not.  The array needs no clearing between calls.
+ * stream do not.  The array needs no clearing between calls.  The array's device
+ * address is looked up on the first call on each device, which must not be inside a
+ * graph capture: such a first call returns KVP_EINVAL before any launch.  After one
+ * call outside capture the entry point may be captured and replayed with new metadata
+ * in the same buffers.
  */
 int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
                                   const void* k_cache, const void* v_cache,
@@ -193,9 +199,10 @@ int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride, int64_t q
  *                         outside [0, num_cache_blocks) or klen_s larger than
  *                         max_blocks_per_seq * block_size makes that sequence's
  *                         output NaN.  block_size must be a multiple of 64.
- * max_seqlen_q bounds every qlen_s (it sizes the grid); sequences longer than it
- * produce NaN.  Replaces flash_attn_varlen_func(..., causal=True, block_table)
- * (flash_attention_kvcache.py:76-79).
+ * max_seqlen_q only sizes the grid: a sequence longer than it is still computed in
+ * full (its extra query tiles are taken by the workgroups that own its first ones), so
+ * an understated max_seqlen_q costs time, never rows.  Replaces
+ * flash_attn_varlen_func(..., causal=True, block_table) (flash_attention_kvcache.py:76-79).
  */
 int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                             const void* k, int64_t k_block_stride, int64_t k_tok_stride,

@@ -920,7 +920,10 @@ static __device__ __align__(256) char scratch[kScratchBytes];
 
 // Device address of this device's `scratch`, looked up once per device with that device
 // current.  The host-side symbol is not a device address and is never passed to a kernel.
-static int scratch_address(const char* fn, char** out) {
+// The lookup may load the library's code object (and the array) on that device, which is
+// not an operation to record into a graph: a first call on a device while `stream` is
+// being captured is refused, and one call outside capture (any batch) sets the device up.
+static int scratch_address(const char* fn, hipStream_t stream, char** out) {
   constexpr int kMaxDevices = 64;
   static std::atomic<char*> addr[kMaxDevices];
   int dev = -1;
@@ -929,6 +932,15 @@ static int scratch_address(const char* fn, char** out) {
   if (dev < 0 || dev >= kMaxDevices) return fail(KVP_EINVAL, "%s: device %d beyond %d", fn, dev, kMaxDevices);
   char* ptr = addr[dev].load(std::memory_order_acquire);
   if (!ptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(stream, &cap);
+    if (err != hipSuccess)
+      return fail(static_cast<int>(err), "%s: hipStreamIsCapturing: %s", fn, hipGetErrorString(err));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(KVP_EINVAL,
+                  "%s: first call on device %d is inside a graph capture; call it once outside capture "
+                  "(any batch) to set up the device's static scratch, then capture",
+                  fn, dev);
     void* sym = nullptr;
     err = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
     if (err != hipSuccess || !sym)
@@ -1015,7 +1027,7 @@ extern "C" int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride
                 "holds %zu (use kvp_paged_decode_bf16 with a caller workspace)",
                 fn, std::min(num_seqs, kMaxSeqsPerLaunch), num_q_heads, static_cast<long long>(need), kScratchBytes);
   char* ws = nullptr;
-  rc = scratch_address(fn, &ws);
+  rc = scratch_address(fn, static_cast<hipStream_t>(stream), &ws);
   if (rc != KVP_OK) return rc;
   return enqueue_decode<false>(fn, a, ranges, ws, static_cast<hipStream_t>(stream));
 }

@@ -97,7 +97,7 @@ def _attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
     G = q.shape[0] // k.shape[0]
     k = k.repeat_interleave(G, dim=0)
     v = v.repeat_interleave(G, dim=0)
-    s = torch.matmul(q, k.transpose(1, 2)) * scale
+    s = torch.matmul(q, k.transpose(1, 2).contiguous()) * scale
     if mask is not None:
         s = s.masked_fill(~mask, float("-inf"))
     any_visible = torch.isfinite(s).any(dim=-1, keepdim=True)
@@ -114,10 +114,11 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     q [B, Hq, D]; caches [num_blocks, block_size, Hkv, D]; block_tables int [B, W];
     context_lens int [B] (tokens including the one just appended).  Returns [B, Hq, D]
     in `dtype`; a zero-length context returns zeros.  Block-table entries past
-    ceil(ctx / block_size) are never read.
+    ceil(ctx / block_size) are never read.  Runs on the device of its inputs (all on one
+    device), so full-size checks can evaluate it in float32 on the GPU.
     """
     B, Hq, D = q.shape
-    out = torch.zeros(B, Hq, D, dtype=dtype)
+    out = torch.zeros(B, Hq, D, dtype=dtype, device=q.device)
     for b in range(B):
         ctx = int(context_lens[b])
         if ctx <= 0:
@@ -136,10 +137,11 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
     q [Tq, Hq, D].  Dense mode (block_tables None): k / v [Tk, Hkv, D], sequence s owns
     rows cu_seqlens_k[s]:cu_seqlens_k[s+1].  Paged mode: k / v are caches and sequence s
-    reads its klen_s logical tokens through block_tables[s].  Returns [Tq, Hq, D].
+    reads its klen_s logical tokens through block_tables[s].  Returns [Tq, Hq, D] on the
+    device of q (inputs on one device; the cu_seqlens may be on the host or the device).
     """
     Tq, Hq, D = q.shape
-    out = torch.zeros(Tq, Hq, D, dtype=dtype)
+    out = torch.zeros(Tq, Hq, D, dtype=dtype, device=q.device)
     cq = [int(x) for x in cu_seqlens_q]
     ck = [int(x) for x in cu_seqlens_k]
     for s in range(len(cq) - 1):
@@ -156,8 +158,8 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         vs = vs.to(dtype).transpose(0, 1)
         mask = None
         if causal:
-            i = torch.arange(qlen).unsqueeze(1)
-            j = torch.arange(klen).unsqueeze(0)
+            i = torch.arange(qlen, device=q.device).unsqueeze(1)
+            j = torch.arange(klen, device=q.device).unsqueeze(0)
             mask = j <= i + (klen - qlen)
         out[cq[s]:cq[s + 1]] = _attend(qs, ks, vs, scale, mask).transpose(0, 1)
     return out

@@ -143,14 +143,11 @@ def test_invalid_block_poisons_only_its_sequence(cuda_device):
     torch.testing.assert_close(out[50:], want[50:], **TOL)
 
 
-def test_full_size_prefix_shared_sampled(cuda_device):
-    """32 sequences, 100-1024 new tokens each, cached prefixes of 0-4096 tokens in whole
-    256-token blocks shared by groups of 4 (identical leading block ids), Qwen3-0.6B heads.
-    All outputs finite; 4 sequences checked against the oracle."""
-    g = gen(250)
-    bs, hkv, hq, d = 256, 8, 16, cuda_device
+def _config_d(g, nb=4096, bs=256):
+    """32 sequences in 8 groups of 4: each group shares a cached prefix of 0-4096 tokens in
+    whole 256-token blocks (identical leading block ids), each sequence 100-1024 new tokens
+    in its own blocks."""
     qlens, prefix, tables = [], [], []
-    nb = 4096
     perm = torch.randperm(nb, generator=g).tolist()
     pos = 0
     for grp in range(8):
@@ -166,24 +163,66 @@ def test_full_size_prefix_shared_sampled(cuda_device):
             tables.append(shared + own)
     width = max(len(t) for t in tables)
     bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.int32)
+    return qlens, prefix, bt
+
+
+def _device_oracle_prefill(q, k, v, cq, ck, out, bt=None):
+    """Every sequence against the fp32 oracle, evaluated on the device in float32."""
+    allow = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        cqh, ckh = cq.tolist(), ck.tolist()
+        for s in range(len(cqh) - 1):
+            r0, r1 = cqh[s], cqh[s + 1]
+            if bt is None:
+                want = ref.varlen_prefill(q[r0:r1], k[ckh[s]:ckh[s + 1]], v[ckh[s]:ckh[s + 1]],
+                                          _cu([r1 - r0]), _cu([ckh[s + 1] - ckh[s]]), SCALE)
+            else:
+                want = ref.varlen_prefill(q[r0:r1], k, v, _cu([r1 - r0]), _cu([ckh[s + 1] - ckh[s]]), SCALE,
+                                          block_tables=bt[s:s + 1])
+            torch.testing.assert_close(out[r0:r1].float(), want, **TOL, msg=lambda m: f"sequence {s}: {m}")
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = allow
+
+
+def test_full_size_prefix_shared_every_sequence(cuda_device):
+    """The prefix-cached prefill workload at full size (32 sequences, 100-1024 new tokens,
+    prefixes of 0-4096 tokens shared by groups of 4, Qwen3-0.6B heads).  Every sequence is
+    compared with the fp32 oracle, so a unit ranked or dealt wrongly for some sequences of
+    the real batch fails here."""
+    g = gen(250)
+    bs, hkv, hq, d, nb = 256, 8, 16, cuda_device, 4096
+    qlens, prefix, bt = _config_d(g, nb, bs)
     cq, ck = _cu(qlens), _cu([a + b for a, b in zip(qlens, prefix)])
     dg = torch.Generator(device=d).manual_seed(250)
     kc = torch.randn(nb, bs, hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
     vc = torch.randn(nb, bs, hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
     q = randn_bf16((sum(qlens), hq, 128), g).to(d)
-    out = _prefill(q, kc, vc, cq.to(d), ck.to(d), max(qlens), bt=bt.to(d))
+    bt_d = bt.to(d)
+    out = _prefill(q, kc, vc, cq.to(d), ck.to(d), max(qlens), bt=bt_d)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    for s in (0, 5, 17, 31):
-        klen = int(ck[s + 1] - ck[s])
-        nblk = math.ceil(klen / bs)
-        sel = bt[s, :nblk].long().to(d)
-        out_s = ref.varlen_prefill(q[cq[s]:cq[s + 1]].cpu(), kc[sel].cpu(), vc[sel].cpu(),
-                                   _cu([qlens[s]]), _cu([klen]), SCALE,
-                                   block_tables=torch.arange(nblk, dtype=torch.int32).view(1, -1))
-        torch.testing.assert_close(out[cq[s]:cq[s + 1]].cpu().float(), out_s, **TOL)
+    _device_oracle_prefill(q, kc, vc, cq, ck, out, bt=bt_d)
     del kc, vc
     torch.cuda.empty_cache()
+
+
+def test_full_size_dense_every_sequence(cuda_device):
+    """The same 32 sequences' new tokens without prefixes, dense k / v rows (the no-prefix
+    batches of the reference's caller, block_table None): every sequence against the
+    fp32 oracle."""
+    g = gen(251)
+    hkv, hq, d = 8, 16, cuda_device
+    qlens, _, _ = _config_d(g)
+    cq = _cu(qlens)
+    dg = torch.Generator(device=d).manual_seed(251)
+    q = torch.randn(sum(qlens), hq, 128, generator=dg, device=d, dtype=torch.bfloat16)
+    k = torch.randn(sum(qlens), hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
+    v = torch.randn(sum(qlens), hkv, 128, generator=dg, device=d, dtype=torch.bfloat16)
+    out = _prefill(q, k, v, cq.to(d), cq.to(d), max(qlens))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    _device_oracle_prefill(q, k, v, cq, cq, out)
 
 
 def test_prefill_golden(cuda_device):
