@@ -89,6 +89,33 @@ def prefill_flops(cu_seqlens_q, cu_seqlens_k, num_q_heads: int, head_dim: int) -
     return 4 * num_q_heads * head_dim * pairs
 
 
+def prefill_bytes(cu_seqlens_q, cu_seqlens_k, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                  block_tables=None, block_size: int = 0) -> int:
+    """Algorithmic HBM bytes of one varlen prefill call: q read and o written once
+    (Tq * Hq * D * 2 each), every distinct key's K and V row read once (Hkv * D * 2 each;
+    with block tables a (block, slot) shared by several sequences counts once, as the
+    prefix pages of a group), plus 4 bytes per cu_seqlens entry and block-table entry."""
+    cq = [int(x) for x in cu_seqlens_q]
+    ck = [int(x) for x in cu_seqlens_k]
+    tq = cq[-1] - cq[0]
+    if block_tables is None:
+        keys = ck[-1] - ck[0]
+        entries = 0
+    else:
+        seen = set()
+        entries = 0
+        for s in range(len(cq) - 1):
+            klen = ck[s + 1] - ck[s]
+            nblk = -(-klen // block_size)
+            entries += nblk
+            for b in range(nblk):
+                blk = int(block_tables[s][b])
+                seen.update((blk, i) for i in range(min(block_size, klen - b * block_size)))
+        keys = len(seen)
+    return (2 * tq * num_q_heads * head_dim * 2 + 2 * keys * num_kv_heads * head_dim * 2
+            + 4 * (len(cq) + len(ck)) + 4 * entries)
+
+
 # ----------------------------------------------------------------------------- inputs
 
 def decode_inputs(dev, B, hq, hkv, lo, hi, pool_blocks, seed=0):
@@ -452,7 +479,9 @@ def bench_prefill(dev, steps, warmup, dense: bool = False):
     warm_for(step, 0.5)
     ms = time_median(step, steps, warmup)
     flops = prefill_flops(cq.cpu().tolist(), ck.cpu().tolist(), hq, D)
-    return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9)
+    nbytes = prefill_bytes(cq.cpu().tolist(), ck.cpu().tolist(), hq, hkv, D,
+                           None if dense else tables, BS)
+    return dict(ms=ms, flops=flops, tflops=flops / ms / 1e9, bytes=nbytes, gbs=nbytes / ms / 1e6)
 
 
 def _median_runs(fn, budget_s: float, min_runs: int = 3, max_runs: int = 50) -> tuple[float, int]:
@@ -661,12 +690,19 @@ def run_extras(dev, steps: int, warmup: int, cpu_baseline: bool = False) -> dict
     torch.cuda.empty_cache()
     p = bench_prefill(dev, *n["prefill"])
     extras["varlen_prefill"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                    ms=round(p["ms"], 4), flops=p["flops"],
+                                    ms=round(p["ms"], 4), flops=p["flops"], bytes=p["bytes"],
+                                    intensity_flop_per_byte=round(p["flops"] / p["bytes"], 1),
+                                    hbm_gbs=round(p["gbs"], 1), hbm_frac=round(p["gbs"] / HBM_PEAK_GBS, 4),
                                     workload="32 seqs, new 100-1024, prefix 0-4096 shared by groups of 4, 16q/8kv")
     torch.cuda.empty_cache()
     p = bench_prefill(dev, *n["prefill"], dense=True)
+    # below the ridge point (2.5 PFLOP/s / 8 TB/s = 312 flop/B) the HBM bound is the roofline
     extras["varlen_prefill_dense"] = dict(tflops=round(p["tflops"], 1), frac=round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                          ms=round(p["ms"], 4), flops=p["flops"],
+                                          ms=round(p["ms"], 4), flops=p["flops"], bytes=p["bytes"],
+                                          intensity_flop_per_byte=round(p["flops"] / p["bytes"], 1),
+                                          hbm_gbs=round(p["gbs"], 1), hbm_frac=round(p["gbs"] / HBM_PEAK_GBS, 4),
+                                          bound="hbm" if p["flops"] / p["bytes"] < BF16_PEAK_TFLOPS / HBM_PEAK_GBS * 1e3
+                                          else "mfma",
                                           workload="config D's 32 sequences of 100-1024 new tokens without "
                                                    "prefixes, dense k/v rows (block_table None), 16q/8kv")
     torch.cuda.empty_cache()

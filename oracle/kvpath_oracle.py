@@ -29,6 +29,10 @@ Kavor source tree):
   sdpa_varlen_prefill  torch.nn.functional.scaled_dot_product_attention in the
                        reference's compute dtype (bf16), as a PyTorch-eager port of the
                        reference's CUDA path would run on host cores
+  decode_bytes, append_bytes, prefill_flops, prefill_bytes
+                       the algorithmic units of the measurements, counted by explicit
+                       loops (token by token, pair by pair) for tests/test_bench_units.py,
+                       which pins bench.py's closed forms against them
 
 Pinning (tests/test_oracle.py): the reference ships no golden vectors for this path
 (its tests cover other kernels), so every function is pinned by checks that a plausible
@@ -335,3 +339,26 @@ def prefill_flops(cu_seqlens_q, cu_seqlens_k, num_q_heads: int, head_dim: int, c
         for i in range(qlen):
             pairs += max(0, min(klen, i + klen - qlen + 1))
     return 4 * num_q_heads * head_dim * pairs
+
+
+def prefill_bytes(cu_seqlens_q, cu_seqlens_k, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                  block_tables=None, block_size: int = 0) -> int:
+    """Algorithmic HBM bytes of a varlen prefill call, counted token by token: q and o
+    rows (read and written once), each distinct key read once as a K and a V row (with
+    block tables, logical token t of sequence s is the physical (block_tables[s][t // bs],
+    t % bs), so tokens of shared prefix pages count once), and 4 bytes per cu_seqlens
+    entry and per block-table entry the sequences need."""
+    cq = [int(x) for x in cu_seqlens_q]
+    ck = [int(x) for x in cu_seqlens_k]
+    q_rows = sum(cq[s + 1] - cq[s] for s in range(len(cq) - 1))
+    keys = set()
+    entries = 0
+    for s in range(len(ck) - 1):
+        klen = ck[s + 1] - ck[s]
+        for t in range(klen):
+            keys.add((s, t) if block_tables is None else (int(block_tables[s][t // block_size]), t % block_size))
+        if block_tables is not None:
+            entries += (klen + block_size - 1) // block_size
+    row = head_dim * 2
+    return (q_rows * num_q_heads * row * 2 + len(keys) * num_kv_heads * row * 2
+            + 4 * (len(cq) + len(ck)) + 4 * entries)

@@ -45,3 +45,36 @@ def test_prefill_flops_match_oracle():
             cq.append(cq[-1] + q)
             ck.append(ck[-1] + k)
         assert bench.prefill_flops(cq, ck, 16, 128) == ref.prefill_flops(cq, ck, 16, 128)
+
+
+def test_prefill_bytes_match_oracle():
+    rng = random.Random(4)
+    for _ in range(30):
+        bs = rng.choice([64, 256])
+        nseq = rng.randint(1, 8)
+        qlens = [rng.randint(1, 500) for _ in range(nseq)]
+        prefix = [bs * rng.randint(0, 4) for _ in range(nseq)]
+        klens = [q + p for q, p in zip(qlens, prefix)]
+        pool = list(range(200))
+        rng.shuffle(pool)
+        shared = pool[:4]  # every sequence's prefix pages start with the same block ids
+        pos = 4
+        tables = []
+        for p, k in zip(prefix, klens):
+            own = -(-k // bs) - p // bs
+            tables.append(shared[:p // bs] + pool[pos:pos + own])
+            pos += own
+        cq, ck = [0], [0]
+        for q, k in zip(qlens, klens):
+            cq.append(cq[-1] + q)
+            ck.append(ck[-1] + k)
+        assert (bench.prefill_bytes(cq, ck, 16, 8, 128, tables, bs)
+                == ref.prefill_bytes(cq, ck, 16, 8, 128, tables, bs))
+        assert bench.prefill_bytes(cq, cq, 16, 8, 128) == ref.prefill_bytes(cq, cq, 16, 8, 128)
+    # the prefix-cached and dense 32-sequence workloads
+    ql, kl, tables = bench.prefill_workload()
+    cq, ck = [0], [0]
+    for q, k in zip(ql, kl):
+        cq.append(cq[-1] + q)
+        ck.append(ck[-1] + k)
+    assert bench.prefill_bytes(cq, ck, 16, 8, 128, tables, 256) == ref.prefill_bytes(cq, ck, 16, 8, 128, tables, 256)

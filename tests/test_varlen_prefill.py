@@ -335,3 +335,45 @@ def test_more_sequences_than_one_launch(cuda_device, paged):
         want = ref.varlen_prefill(q, k, v, _cu(qlens), _cu(klens), SCALE)
     torch.cuda.synchronize()
     torch.testing.assert_close(out.cpu().float(), want, **TOL)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_rising_scores_rebase_the_running_max(cuda_device, paged):
+    """P is formed against the running max of the query tile's first key tile; later
+    tiles whose scores rise past it re-base the max.  Sequence 0: scores grow by about
+    1.5 (base 2) per 64-key tile over 32 tiles, so the max is re-based every dozen tiles.
+    Sequence 1: keys after the first tile score about 133 (base 2) above the first ones,
+    so exp2 overflows to inf before the re-base.  Both against the oracle."""
+    g = gen(270)
+    u = torch.zeros(128)
+    u[0] = 1.0
+    qlens, klens = [64, 64], [2048, 256]
+    q = (4.0 * u + 0.05 * torch.randn(sum(qlens), 16, 128, generator=g)).to(torch.bfloat16)
+    rise = (3.0 * (torch.arange(2048) // 64).float()).view(-1, 1, 1) * u
+    jump = torch.where(torch.arange(256) < 64, 0.0, 260.0).view(-1, 1, 1) * u
+    k = torch.cat([rise, jump]).expand(-1, 8, 128) + 0.05 * torch.randn(sum(klens), 8, 128, generator=g)
+    k = k.to(torch.bfloat16)
+    v = randn_bf16((sum(klens), 8, 128), g)
+    cq, ck = _cu(qlens), _cu(klens)
+    d = cuda_device
+    want = ref.varlen_prefill(q, k, v, cq, ck, SCALE)
+    if paged:
+        bs, nb = 64, sum(klens) // 64 + 3
+        perm = torch.randperm(nb, generator=g)
+        kc = torch.zeros(nb, bs, 8, 128, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        tables, pos = [], 0
+        for s, kl in enumerate(klens):
+            ids = perm[pos:pos + kl // bs]
+            pos += kl // bs
+            kc[ids] = k[ck[s]:ck[s + 1]].view(-1, bs, 8, 128)
+            vc[ids] = v[ck[s]:ck[s + 1]].view(-1, bs, 8, 128)
+            tables.append(ids.tolist())
+        width = max(len(t) for t in tables)
+        bt = torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.int32)
+        out = _prefill(q.to(d), kc.to(d), vc.to(d), cq.to(d), ck.to(d), 64, bt=bt.to(d))
+    else:
+        out = _prefill(q.to(d), k.to(d), v.to(d), cq.to(d), ck.to(d), 64)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    torch.testing.assert_close(out.cpu().float(), want, **TOL)
