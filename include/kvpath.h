@@ -199,9 +199,12 @@ int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride, int64_t q
  *                         outside [0, num_cache_blocks) or klen_s larger than
  *                         max_blocks_per_seq * block_size makes that sequence's
  *                         output NaN.  block_size must be a multiple of 64.
- * max_seqlen_q only sizes the grid: a sequence longer than it is still computed in
+ * max_seqlen_q only sizes the work list: a sequence longer than it is still computed in
  * full (its extra query tiles are taken by the workgroups that own its first ones), so
- * an understated max_seqlen_q costs time, never rows.  Replaces
+ * an understated max_seqlen_q costs time, never rows.  The workspace (size from
+ * kvp_prefill_workspace_bytes, 256-byte aligned) holds the launch's work list; a smaller
+ * one returns KVP_EWORKSPACE before any launch, and calls that share one workspace must
+ * be ordered on one stream.  Replaces
  * flash_attn_varlen_func(..., causal=True, block_table) (flash_attention_kvcache.py:76-79).
  */
 int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -217,7 +220,20 @@ int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int64_t q_head_
                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                             float softmax_scale, int32_t causal,
                             void* out, int64_t out_tok_stride, int64_t out_head_stride,
-                            void* stream);
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of device workspace kvp_varlen_prefill_bf16 needs for up to num_seqs sequences
+ * whose longest has max_seqlen_q query tokens (num_q_heads / num_kv_heads picks the
+ * tile shape): 2 KiB plus 32 bytes per pair of query tiles per sequence, for at most
+ * 2048 sequences (one launch; larger batches run as consecutive launches on the same
+ * workspace).  Qwen3-0.6B, 256 sequences of up to 4096 tokens: 264 KiB.  The caller
+ * allocates it once (before any graph capture), 256-byte aligned; it needs no
+ * initialisation: every call rewrites what it reads.  Returns 0 for arguments the
+ * prefill does not support.
+ */
+size_t kvp_prefill_workspace_bytes(int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
+                                   int32_t num_kv_heads);
 
 /* ------------------------------------------------------------------------------
  * The layer work on either side of the path (the engine's Qwen3 layers).  Same

@@ -86,8 +86,9 @@ SIGNATURES: dict[str, tuple] = {
         _i32, _i32, _i32,                 # num_q_heads, num_kv_heads, head_dim
         _f32, _i32,                       # softmax_scale, causal
         _c_void_p, _i64, _i64,            # out, out_tok_stride, out_head_stride
-        _c_void_p,                        # stream
+        _c_void_p, _size_t, _c_void_p,    # workspace, workspace_bytes, stream
     ]),
+    "kvp_prefill_workspace_bytes": (_size_t, [_i32, _i32, _i32, _i32]),
     "kvp_rmsnorm_bf16": (ctypes.c_int, [
         _c_void_p, _i64, _i64,            # x, x_stride0, x_stride1
         _c_void_p, _i64, _i64,            # residual, residual_stride0, residual_stride1

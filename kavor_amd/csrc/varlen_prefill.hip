@@ -23,12 +23,11 @@
 //   (v_permlane32_swap, no LDS) and P feeds the second MFMA straight from registers.  The
 //   softmax scale is folded into the exponent (exp2(fma(s, scale*log2 e, -m))).
 //   Q stays in registers for the whole key loop (8 x 16 bytes per lane).
-//   Work order: every workgroup ranks the units of work (a pair of neighbouring query
-//   tiles of one sequence and kv head) by cost and takes the one of its own rank, so
-//   the most expensive units start first and the cheap ones fill in behind them; the
-//   two tiles of a unit run on one XCD.  Dense prefill runs persistent workgroups that
-//   take every grid-th rank, so the many short units of a batch without prefixes do not
-//   each pay a workgroup's start-up.
+//   Work order: a one-workgroup plan kernel ranks the units of work (a pair of
+//   neighbouring query tiles of one sequence and kv head) by cost into a caller
+//   workspace; persistent workgroups (two per CU) then claim them in that order from
+//   per-XCD counters, so the most expensive units start first, the cheap ones fill in
+//   behind them, and the two tiles of a unit run on one XCD.
 #include <math.h>
 
 #include <algorithm>
@@ -44,14 +43,19 @@ constexpr int kPrefillThreads = 64 * kPrefillWaves;
 constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows (token x head) per workgroup
 constexpr int kKeyTile = 64;
 constexpr int kXcdGroup = 2;  // neighbouring query tiles of one (sequence, kv head) per XCD
-// Sequences per launch: their lengths and starts (8 bytes each) are staged in an idle K
-// and an idle V tile buffer before the first tile; larger batches run as consecutive
+// Sequences per launch (the plan kernel's loop bound); larger batches run as consecutive
 // launches.
 constexpr int kMaxPrefillSeqs = 2048;
-static_assert(kKeyTile * kPrefillHeadDim * 2 >= kMaxPrefillSeqs * 8, "lengths must fit one tile buffer");
-// Dense prefill runs persistent workgroups, which keep the lengths in LDS of their own
-// across units: up to 1024 sequences per launch (8 KiB; 72 KiB per workgroup in all).
-constexpr int kMaxDenseSeqs = 1024;
+// Workspace of one launch: the per-XCD claim counters (each on its own 128-byte line),
+// the unit count, then the unit pairs in decreasing cost, 32 bytes each.
+constexpr int kClaimStride = 32;           // ints between claim counters
+constexpr int kWsCountInt = 8 * kClaimStride;  // the unit count (int index)
+constexpr int kWsUnitsInt = 512;           // first unit pair (int index; byte 2048)
+constexpr int kUnitInts = 8;               // s, pair index, q start, q length, k start, k length, 0, 0
+constexpr int kPlanThreads = 256;
+constexpr int kPlanSeqsPerThread = kMaxPrefillSeqs / kPlanThreads;
+constexpr int kPlanLevels = 2048;          // cost levels (64-key tiles) ranked apart; longer units tie at the top
+static_assert(kPlanLevels % kPlanThreads == 0 && kMaxPrefillSeqs % kPlanThreads == 0, "plan shape");
 // A tile's row sum of P above this re-bases the running max (P itself stays <= 2^16).
 constexpr float kSpecSumLimit = 65536.f;
 
@@ -78,7 +82,87 @@ struct PrefillParams {
   float scale_log2;
   uint16_t* out;
   int64_t o_tok_stride, o_head_stride;
+  int* ws;  // launch workspace: claim counters, unit count, ranked unit pairs
 };
+
+// Ranks the launch's units by cost for the persistent attention workgroups.  A unit is a
+// pair of neighbouring query tiles of one (sequence, kv head); its cost is the key-tile
+// count of its later (longer) tile, ceil(min(kl, min(ql, (i + 1) TOK) + kl - ql) / 64)
+// for tile i (kl without the causal mask), and unit j of a sequence with ntl query tiles
+// starts at tile ntl - 1 - 2j (j < J; J = pair_slots covers max_seqlen_q).  One workgroup
+// histograms the (sequence, j) pairs by cost, turns the histogram into offsets in
+// decreasing cost and places each pair; every kv head of a pair follows it in rank order.
+// It also zeroes the claim counters, so a workspace needs no clearing.  Pairs of one cost
+// are placed in no fixed order: the attention outputs do not depend on the order.
+template <int G, bool CAUSAL>
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const PrefillParams p) {
+  constexpr int TOK = kPrefillRows / G;
+  __shared__ int hist[kPlanLevels];
+  __shared__ int wsum[kPlanThreads / 64];
+  __shared__ int total;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kPlanLevels; i += kPlanThreads) hist[i] = 0;
+  if (tid < 8) p.ws[kClaimStride * tid] = 0;
+  if (tid == 0) total = 0;
+  __syncthreads();
+  const int J = p.pair_slots;
+  auto level = [&](int ql, int kl, int j) {
+    const int i = (ql + TOK - 1) / TOK - 1 - 2 * j;
+    const int e = CAUSAL ? min(kl, min(ql, (i + 1) * TOK) + kl - ql) : kl;
+    return min(max((e + kKeyTile - 1) / kKeyTile, 0), kPlanLevels - 1);
+  };
+  int q0[kPlanSeqsPerThread], ql[kPlanSeqsPerThread], k0[kPlanSeqsPerThread], kl[kPlanSeqsPerThread];
+  int mine = 0;
+#pragma unroll
+  for (int u = 0; u < kPlanSeqsPerThread; ++u) {
+    const int sq = tid + kPlanThreads * u;
+    q0[u] = ql[u] = k0[u] = kl[u] = 0;
+    if (sq < p.num_seqs) {
+      q0[u] = p.cu_q[sq];
+      ql[u] = p.cu_q[sq + 1] - q0[u];
+      k0[u] = p.cu_k[sq];
+      kl[u] = p.cu_k[sq + 1] - k0[u];
+    }
+    const int nu = min(J, ((ql[u] + TOK - 1) / TOK + 1) / 2);
+    for (int j = 0; j < nu; ++j) atomicAdd(&hist[level(ql[u], kl[u], j)], 1);
+    mine += nu;
+  }
+  if (mine) atomicAdd(&total, mine);
+  __syncthreads();
+  // exclusive offsets in decreasing cost: thread t owns the kPlanLevels / kPlanThreads
+  // levels just below the ones of thread t - 1
+  constexpr int LPT = kPlanLevels / kPlanThreads;
+  const int top = kPlanLevels - 1 - LPT * tid;
+  int h[LPT], run = 0;
+#pragma unroll
+  for (int e = 0; e < LPT; ++e) {
+    h[e] = hist[top - e];
+    run += h[e];
+  }
+  const int incl = wave_incl_scan(run);
+  if ((tid & 63) == 63) wsum[tid >> 6] = incl;
+  __syncthreads();
+  int before = incl - run;
+  for (int w = 0; w < (tid >> 6); ++w) before += wsum[w];
+#pragma unroll
+  for (int e = 0; e < LPT; ++e) {
+    hist[top - e] = before;
+    before += h[e];
+  }
+  __syncthreads();
+  int* units = p.ws + kWsUnitsInt;
+#pragma unroll
+  for (int u = 0; u < kPlanSeqsPerThread; ++u) {
+    const int sq = tid + kPlanThreads * u;
+    const int nu = min(J, ((ql[u] + TOK - 1) / TOK + 1) / 2);
+    for (int j = 0; j < nu; ++j) {
+      const int pos = atomicAdd(&hist[level(ql[u], kl[u], j)], 1);
+      *reinterpret_cast<int4*>(units + kUnitInts * pos) = make_int4(sq, j, q0[u], ql[u]);
+      *reinterpret_cast<int4*>(units + kUnitInts * pos + 4) = make_int4(k0[u], kl[u], 0, 0);
+    }
+  }
+  if (tid == 0) p.ws[kWsCountInt] = total * p.num_kv_heads;
+}
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
@@ -116,25 +200,18 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   constexpr int D = kPrefillHeadDim;
   constexpr int TOK = kPrefillRows / G;  // query tokens per tile
 
-  // Work order.  A unit is a pair of neighbouring query tiles of one (sequence, kv
-  // head); its cost is the key-tile count of its longer (later) tile.  Workgroup pair
-  // (b, b + 8) takes the unit of rank m in decreasing cost: the hardware deals
-  // workgroup ids round-robin to the 8 XCDs, so the two tiles, which read nearly the
-  // same K/V, run together on one XCD and share its L2 (0.53 -> 0.50 ms on the
-  // prefix-cached 32-sequence workload).  The most expensive units start first and the
-  // cheap ones fill in behind them: 0.82 -> 0.58 ms for "last tiles first" against
-  // (sequence, kv head, tile) order, and 0.457 -> 0.437 ms for the global cost order
-  // against "last tiles first".  The rank is found by a binary search over cost levels
-  // on closed-form unit counts per sequence (no sort, no workspace).
-  int b = blockIdx.x;
-  int m0 = (b / (8 * kXcdGroup)) * 8 + (b % 8);  // this workgroup pair's rank
-  int member = (b % (8 * kXcdGroup)) / 8;        // which tile of the unit
-  // Dense: persistent workgroups.  Workgroup b takes the units of ranks m0(b),
-  // m0(b + grid), ... (the grid is a multiple of 16, so b + k grid keeps b's XCD and pair
-  // member).  Paged: one unit per workgroup, placed by the hardware's dispatch, which
-  // balances the very unequal units of prefix-cached batches better than a static deal.
-  constexpr bool PERSIST = !PAGED;
-  const int nseq = p.num_seqs;
+  // Work order.  The plan kernel listed the units in decreasing cost; persistent
+  // workgroups claim them in that order, so the most expensive units start first and the
+  // cheap ones fill in behind them (0.82 -> 0.58 ms for "last tiles first" against
+  // (sequence, kv head, tile) order, then 0.457 -> 0.437 ms for the global cost order,
+  // one workgroup per unit).  Claims come from one counter per XCD: workgroup b runs on
+  // XCD b % 8 (the hardware deals workgroup ids round-robin to the 8 XCDs), claim c of
+  // XCD x is rank 8 (c / 2) + x, and its two tiles go to two consecutive claims, so both
+  // tiles of a unit, which read nearly the same K/V, run together on one XCD and share its
+  // L2 (0.53 -> 0.50 ms).  Against one workgroup per unit with an in-kernel rank search:
+  // prefix-cached 32-sequence prefill 365.5 -> 361.4 us, its dense form 96.1 -> 91.4 us
+  // (plan kernel included; the persistent workgroups need no per-unit search, no
+  // per-workgroup staging of the lengths and no empty workgroups).
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases and M0 stay scalar
   const int lane = tid & 63;
@@ -146,131 +223,35 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   __shared__ __attribute__((aligned(16))) uint16_t s_k0[kKeyTile * kPrefillHeadDim];
   __shared__ __attribute__((aligned(16))) uint16_t s_k1[kKeyTile * kPrefillHeadDim];
   __shared__ __attribute__((aligned(16))) uint16_t s_v0[kKeyTile * kPrefillHeadDim];
-  // (dense: the lengths, kept across units, follow the last tile buffer)
-  __shared__ __attribute__((aligned(16))) uint16_t s_v1[kKeyTile * kPrefillHeadDim + (PERSIST ? 4 * kMaxDenseSeqs : 0)];
-
-  // Before the first K/V tile is staged, the K buffers hold every sequence's
-  // (query length, key length) and the V buffers its (query start, key start).
-  int2* s_len = reinterpret_cast<int2*>(PERSIST ? &s_v1[kKeyTile * kPrefillHeadDim] : &s_k0[0]);
-  int2* s_start = reinterpret_cast<int2*>(&s_v0[0]);  // paged only
-  const int J = p.pair_slots;  // tile pairs per (sequence, kv head) the grid covers
-
-  // Units of sequence (ql, kl) whose first tile needs at least L key tiles.  Tile i of
-  // TOK query tokens needs ceil(min(kl, min(ql, (i+1) TOK) + kl - ql) / 64) key tiles,
-  // which grows with i; unit j (< J) starts with tiles ntl-1-2j and ntl-2-2j.
-  auto units_ge = [&](int ql, int kl, int L) -> int {
-    const int ntl = (ql + TOK - 1) / TOK;
-    if (ntl == 0) return 0;
-    const int all = min(J, (ntl + 1) / 2);
-    if (L <= 0) return all;
-    const int x = kKeyTile * (L - 1);
-    if (kl <= x) return 0;
-    if (!CAUSAL) return all;
-    const int y = x - (kl - ql);
-    const int fi = y <= 0 ? 0 : y / TOK;
-    return min(all, (ntl - 1 - fi) / 2 + 1);
-  };
-  // Sum / maximum over the wave by DPP inside 16-lane rows and the gfx950 row and half
-  // swaps (VALU only; the LDS-routed shuffles cost a round trip each), with the first 64
-  // sequences' lengths kept in registers across the search: 398.5 -> 390.7 us on the
-  // prefix-cached 32-sequence workload, dense 104.1 -> 101.2 us, same outputs.
-  auto wave_sum = [&](int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, kDppQuadXor1, 0xf, 0xf, false);
-    v += __builtin_amdgcn_update_dpp(0, v, kDppQuadXor2, 0xf, 0xf, false);
-    v += __builtin_amdgcn_update_dpp(0, v, kDppRowHalfMirror, 0xf, 0xf, false);
-    v += __builtin_amdgcn_update_dpp(0, v, kDppRowMirror, 0xf, 0xf, false);
-    auto r = __builtin_amdgcn_permlane16_swap(static_cast<u32>(v), static_cast<u32>(v), false, false);
-    v = static_cast<int>(r[0] + r[1]);
-    r = __builtin_amdgcn_permlane32_swap(static_cast<u32>(v), static_cast<u32>(v), false, false);
-    return static_cast<int>(r[0] + r[1]);
-  };
-  auto wave_max = [&](int v) {
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppQuadXor1, 0xf, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppQuadXor2, 0xf, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppRowHalfMirror, 0xf, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppRowMirror, 0xf, 0xf, false));
-    auto r = __builtin_amdgcn_permlane16_swap(static_cast<u32>(v), static_cast<u32>(v), false, false);
-    v = max(static_cast<int>(r[0]), static_cast<int>(r[1]));
-    r = __builtin_amdgcn_permlane32_swap(static_cast<u32>(v), static_cast<u32>(v), false, false);
-    return max(static_cast<int>(r[0]), static_cast<int>(r[1]));
-  };
-  int2 len_lane = make_int2(0, 0);  // the first 64 sequences' lengths, one per lane
-  auto count_ge = [&](int L) {
-    int c = units_ge(len_lane.x, len_lane.y, L);
-    for (int i = lane + 64; i < nseq; i += 64) {
-      const int2 l = s_len[i];
-      c += units_ge(l.x, l.y, L);
-    }
-    return wave_sum(c) * p.num_kv_heads;
-  };
-
-  for (int i = tid; i < nseq; i += kPrefillThreads) {
-    const int q0s = p.cu_q[i], q1s = p.cu_q[i + 1], k0s = p.cu_k[i], k1s = p.cu_k[i + 1];
-    s_len[i] = make_int2(q1s - q0s, k1s - k0s);
-    if (!PERSIST) s_start[i] = make_int2(q0s, k0s);
-  }
+  __shared__ __attribute__((aligned(16))) uint16_t s_v1[kKeyTile * kPrefillHeadDim];
+  // Each unit's next claim is published in the slot of its unit count's parity: a slot is
+  // rewritten two units later, after a barrier every wave has passed since reading it.
+  __shared__ int s_claim[2];
+  const int J = p.pair_slots;  // tile pairs per (sequence, kv head) the plan covers
+  const int xcd = blockIdx.x & 7;
+  int* const ctr = p.ws + kClaimStride * xcd;
+  const int num_units = __builtin_amdgcn_readfirstlane(p.ws[kWsCountInt]);
+  if (tid == 0) s_claim[0] = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (lane < nseq) len_lane = s_len[lane];
-  const int total_units = count_ge(0);
+  int claim = __builtin_amdgcn_readfirstlane(s_claim[0]);
+  int cslot = 1;
 
   for (;;) {
-  // Rank r in the order of decreasing cost (ties: sequence, kv head, unit).  Every wave
-  // computes the same answer.
-  const int r = m0;
-  if (r >= total_units) break;  // uniform; no barrier follows
-  int kmax = len_lane.y;
-  for (int i = lane + 64; i < nseq; i += 64) kmax = max(kmax, s_len[i].y);
-  int lo = 0, hi = (wave_max(kmax) + kKeyTile - 1) / kKeyTile + 1, c_hi = 0;
-  while (hi - lo > 1) {  // count_ge(lo) > r >= count_ge(hi) = c_hi
-    const int mid = (lo + hi) >> 1;
-    const int c = count_ge(mid);
-    if (c > r) lo = mid;
-    else { hi = mid; c_hi = c; }
-  }
-  int rr = r - c_hi;  // rank among the units of cost level lo
-  int s = -1, e_s = 1, skip = 0;
-  for (int base = 0; base < nseq; base += 64) {
-    const int i = base + lane;
-    int e = 0, ghi = 0;
-    if (i < nseq) {
-      const int2 l = base == 0 ? len_lane : s_len[i];
-      ghi = units_ge(l.x, l.y, lo + 1);
-      e = (units_ge(l.x, l.y, lo) - ghi) * p.num_kv_heads;
-    }
-    int incl = e;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(incl, o);
-      if (lane >= o) incl += t;
-    }
-    const int tot = __shfl(incl, 63);
-    if (rr < tot) {
-      const unsigned long long hit = __ballot(incl > rr);
-      const int w = __builtin_ctzll(hit);
-      s = base + w;
-      e_s = __shfl(e, w);
-      skip = __shfl(ghi, w);
-      rr -= __shfl(incl - e, w);
-      break;
-    }
-    rr -= tot;
-  }
-  if (s < 0 || rr < 0 || rr >= e_s) break;  // unreachable while the counts agree (uniform)
-  // Every lane holds the same values: readfirstlane keeps them (and the addresses
-  // derived from them) in scalar registers.
-  s = __builtin_amdgcn_readfirstlane(s);
-  const int per_head = __builtin_amdgcn_readfirstlane(e_s) / p.num_kv_heads;
-  rr = __builtin_amdgcn_readfirstlane(rr);
-  const int kvh = rr / per_head;
-  const int jj = __builtin_amdgcn_readfirstlane(skip) + rr % per_head;
-  const int2 ls = s_len[s];
-  const int2 st = PERSIST ? make_int2(p.cu_q[s], p.cu_k[s]) : s_start[s];
-  const int q_start = __builtin_amdgcn_readfirstlane(st.x);
-  const int qlen = __builtin_amdgcn_readfirstlane(ls.x);
-  const int k_start = __builtin_amdgcn_readfirstlane(st.y);
-  const int klen = __builtin_amdgcn_readfirstlane(ls.y);
+  const int r = 8 * (claim >> 1) + xcd;  // rank in decreasing cost
+  const int member = claim & 1;          // which tile of the unit
+  if (r >= num_units) break;             // uniform
+  const int* ent = p.ws + kWsUnitsInt + kUnitInts * (r / p.num_kv_heads);
+  const int kvh = r % p.num_kv_heads;
+  const int s = __builtin_amdgcn_readfirstlane(ent[0]);
+  const int jj = __builtin_amdgcn_readfirstlane(ent[1]);
+  const int q_start = __builtin_amdgcn_readfirstlane(ent[2]);
+  const int qlen = __builtin_amdgcn_readfirstlane(ent[3]);
+  const int k_start = __builtin_amdgcn_readfirstlane(ent[4]);
+  const int klen = __builtin_amdgcn_readfirstlane(ent[5]);
   const int diag = klen - qlen;  // bottom-right causal offset
-  if (!PERSIST) __syncthreads();  // every wave has read the lengths: the buffers may be staged
+  // the next claim: issued now, published at the end of this unit
+  int next_claim = 0;
+  if (tid == 0) next_claim = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   bool bad = false;
   if (PAGED && klen > p.max_blocks * p.block_size) bad = true;
@@ -679,10 +660,10 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         }
     }
   }
-  if (!PERSIST) break;
-  b += gridDim.x;
-  m0 = (b / (8 * kXcdGroup)) * 8 + (b % 8);
-  member = (b % (8 * kXcdGroup)) / 8;
+  if (tid == 0) s_claim[cslot] = next_claim;
+  __syncthreads();
+  claim = __builtin_amdgcn_readfirstlane(s_claim[cslot]);
+  cslot ^= 1;
   }  // next unit
 }
 
@@ -708,24 +689,36 @@ static int64_t prefill_resident() {
   return v;
 }
 
-// `total` is the unit-pair slot count rounded up to a multiple of 16: one workgroup per
-// slot (paged), or the resident count of persistent workgroups if smaller (dense).
+// The plan kernel ranks the launch's units into the workspace, then the resident count of
+// persistent workgroups (a multiple of 16, so each XCD holds the same number) claims them.
 template <int G, bool PAGED, bool CAUSAL>
-static void launch_variant(int64_t total, hipStream_t s, const PrefillParams& p) {
-  const int64_t grid = PAGED ? total : std::min<int64_t>(total, prefill_resident<G, PAGED, CAUSAL>());
+static void launch_variant(hipStream_t s, const PrefillParams& p) {
+  hipLaunchKernelGGL((prefill_plan_kernel<G, CAUSAL>), dim3(1), dim3(kPlanThreads), 0, s, p);
+  const int64_t grid = prefill_resident<G, PAGED, CAUSAL>();
   hipLaunchKernelGGL((varlen_prefill_kernel<G, PAGED, CAUSAL>), dim3(static_cast<unsigned>(grid)),
                      dim3(kPrefillThreads), 0, s, p);
 }
 
 template <int G>
-static void launch_prefill(bool paged, bool causal, int64_t total, hipStream_t s, const PrefillParams& p) {
+static void launch_prefill(bool paged, bool causal, hipStream_t s, const PrefillParams& p) {
   if (paged) {
-    if (causal) launch_variant<G, true, true>(total, s, p);
-    else launch_variant<G, true, false>(total, s, p);
+    if (causal) launch_variant<G, true, true>(s, p);
+    else launch_variant<G, true, false>(s, p);
   } else {
-    if (causal) launch_variant<G, false, true>(total, s, p);
-    else launch_variant<G, false, false>(total, s, p);
+    if (causal) launch_variant<G, false, true>(s, p);
+    else launch_variant<G, false, false>(s, p);
   }
+}
+
+// Tile pairs per (sequence, kv head) that cover max_seqlen_q query tokens at GQA ratio g.
+static int64_t prefill_pair_slots(int64_t max_seqlen_q, int g) {
+  const int64_t tok_per_tile = kPrefillRows / g;
+  return ((max_seqlen_q + tok_per_tile - 1) / tok_per_tile + kXcdGroup - 1) / kXcdGroup;
+}
+
+// Workspace bytes of one launch over up to `seqs` sequences.
+static int64_t prefill_workspace_need(int64_t seqs, int64_t pair_slots) {
+  return 4 * static_cast<int64_t>(kWsUnitsInt) + 4 * kUnitInts * seqs * pair_slots;
 }
 
 }  // namespace kvp
@@ -745,7 +738,7 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
                                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                                        float softmax_scale, int32_t causal,
                                        void* out, int64_t out_tok_stride, int64_t out_head_stride,
-                                       void* stream) {
+                                       void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (num_seqs < 0 || max_seqlen_q < 0)
     return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: num_seqs=%d max_seqlen_q=%d", num_seqs, max_seqlen_q);
@@ -785,11 +778,15 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
     return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: k/v token strides %lld / %lld out of range",
                 static_cast<long long>(k_tok_stride), static_cast<long long>(v_tok_stride));
 
-  const int tok_per_tile = kPrefillRows / G;
-  const int64_t num_tiles = (static_cast<int64_t>(max_seqlen_q) + tok_per_tile - 1) / tok_per_tile;
-  const int64_t pair_slots = (num_tiles + kXcdGroup - 1) / kXcdGroup;
+  const int64_t pair_slots = prefill_pair_slots(max_seqlen_q, G);
   if (pair_slots * num_kv_heads * kMaxPrefillSeqs * kXcdGroup > (1ll << 30))
-    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: grid too large");
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: too many units of work (max_seqlen_q=%d)", max_seqlen_q);
+  const int64_t need = prefill_workspace_need(std::min(num_seqs, kMaxPrefillSeqs), pair_slots);
+  if (!workspace || workspace_bytes < static_cast<size_t>(need))
+    return fail(KVP_EWORKSPACE, "kvp_varlen_prefill_bf16: workspace of %zu bytes, %lld needed", workspace_bytes,
+                static_cast<long long>(need));
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: workspace must be 256-byte aligned");
 
   PrefillParams p;
   p.q = static_cast<const uint16_t*>(q);
@@ -813,29 +810,38 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
   p.out = static_cast<uint16_t*>(out);
   p.o_tok_stride = out_tok_stride;
   p.o_head_stride = out_head_stride;
+  p.ws = static_cast<int*>(workspace);
 
-  constexpr int64_t kRound = 8 * kXcdGroup;  // one group on each of the 8 XCDs
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool c = causal != 0;
   // cu_seqlens hold absolute offsets, so a launch over sequences [s0, s0 + n) reads
-  // the same q/k/out rows through the offset pointers.
-  const int chunk = paged ? kMaxPrefillSeqs : kMaxDenseSeqs;
-  for (int s0 = 0; s0 < num_seqs; s0 += chunk) {
-    const int n = std::min(chunk, num_seqs - s0);
+  // the same q/k/out rows through the offset pointers.  Consecutive launches share the
+  // workspace: each one's plan kernel runs after the previous attention kernel.
+  for (int s0 = 0; s0 < num_seqs; s0 += kMaxPrefillSeqs) {
+    const int n = std::min(kMaxPrefillSeqs, num_seqs - s0);
     p.cu_q = cu_seqlens_q + s0;
     p.cu_k = cu_seqlens_k + s0;
     p.block_tables = paged ? block_tables + s0 * block_table_stride : nullptr;
     p.num_seqs = n;
-    const int64_t total = (pair_slots * num_kv_heads * n * kXcdGroup + kRound - 1) / kRound * kRound;
     switch (G) {
-      case 1: launch_prefill<1>(paged, c, total, s, p); break;
-      case 2: launch_prefill<2>(paged, c, total, s, p); break;
-      case 4: launch_prefill<4>(paged, c, total, s, p); break;
-      case 5: launch_prefill<5>(paged, c, total, s, p); break;
-      default: launch_prefill<8>(paged, c, total, s, p); break;
+      case 1: launch_prefill<1>(paged, c, s, p); break;
+      case 2: launch_prefill<2>(paged, c, s, p); break;
+      case 4: launch_prefill<4>(paged, c, s, p); break;
+      case 5: launch_prefill<5>(paged, c, s, p); break;
+      default: launch_prefill<8>(paged, c, s, p); break;
     }
     const int rc = launch_status("kvp_varlen_prefill_bf16");
     if (rc != KVP_OK) return rc;
   }
   return KVP_OK;
+}
+
+extern "C" size_t kvp_prefill_workspace_bytes(int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
+                                              int32_t num_kv_heads) {
+  if (num_seqs < 0 || max_seqlen_q < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return 0;
+  const int g = num_q_heads / num_kv_heads;
+  if (g != 1 && g != 2 && g != 4 && g != 5 && g != 8) return 0;
+  return static_cast<size_t>(
+      prefill_workspace_need(std::min(num_seqs, kMaxPrefillSeqs), prefill_pair_slots(max_seqlen_q, g)));
 }

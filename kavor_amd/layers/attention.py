@@ -23,6 +23,7 @@ from kavor_amd.utils.context import get_context
 __all__ = [
     "store_kvcache", "paged_decode", "paged_decode_fused", "varlen_prefill", "Attention",
     "reserve_decode_workspace", "decode_workspace_bytes",
+    "reserve_prefill_workspace", "prefill_workspace_bytes",
     "flash_attn_with_kvcache", "flash_attn_varlen_func",
 ]
 
@@ -118,6 +119,38 @@ def reserve_decode_workspace(max_num_seqs: int, num_q_heads: int, head_dim: int,
             _retired_workspaces.append(ws)
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         _workspaces[dev.index] = ws
+    return ws
+
+
+# ----------------------------------------------------------------------------- prefill workspace
+
+_prefill_workspaces: dict[int, torch.Tensor] = {}
+
+
+def prefill_workspace_bytes(num_seqs: int, max_seqlen_q: int, num_q_heads: int, num_kv_heads: int) -> int:
+    return int(lib().kvp_prefill_workspace_bytes(num_seqs, max_seqlen_q, num_q_heads, num_kv_heads))
+
+
+def reserve_prefill_workspace(num_seqs: int, max_seqlen_q: int, num_q_heads: int, num_kv_heads: int,
+                              device: torch.device | str | int) -> torch.Tensor:
+    """Allocates (or grows) the per-device prefill workspace: the work list of a launch
+    (kvp_prefill_workspace_bytes).  A caller that captures prefill into a graph reserves
+    the largest batch first; an eager call that needs more grows the workspace without
+    freeing the one a graph holds."""
+    nbytes = prefill_workspace_bytes(num_seqs, max_seqlen_q, num_q_heads, num_kv_heads)
+    dev = torch.device(device) if not isinstance(device, int) else torch.device("cuda", device)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    ws = _prefill_workspaces.get(dev.index)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "the prefill workspace must be reserved before graph capture "
+                f"({nbytes} bytes needed): call reserve_prefill_workspace() first")
+        if ws is not None:
+            _retired_workspaces.append(ws)
+        ws = torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=dev)
+        _prefill_workspaces[dev.index] = ws
     return ws
 
 
@@ -274,6 +307,7 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen
         bt_ptr, bt_stride, max_blocks = block_table.data_ptr(), block_table.stride(0), block_table.shape[1]
     if k.shape[-1] != D:
         raise ValueError("head_dim mismatch between q and k")
+    ws = reserve_prefill_workspace(num_seqs, int(max_seqlen_q), Hq, Hkv, q.device) if num_seqs else None
     rc = lib().kvp_varlen_prefill_bf16(
         q.data_ptr(), q.stride(0), q.stride(1),
         k.data_ptr(), *kstr,
@@ -281,7 +315,8 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen
         bt_ptr, bt_stride, num_blocks, block_size, max_blocks,
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_q),
         Hq, Hkv, D, float(softmax_scale), 1 if causal else 0,
-        out.data_ptr(), out.stride(0), out.stride(1), _stream(q))
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0, _stream(q))
     check("kvp_varlen_prefill_bf16", rc)
     return out
 

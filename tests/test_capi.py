@@ -148,7 +148,8 @@ def test_decode_workspace_size_formula():
 def _prefill(**over):
     args = dict(q=16, qts=2048, qhs=128, k=16, kbs=0, kts=1024, khs=128, v=16, vbs=0, vts=4096,
                 vhs=128, bt=None, bts=0, nblk=0, bs=0, maxb=0, cuq=16, cuk=16, nseq=2, maxq=100,
-                hq=16, hkv=8, d=128, scale=0.088, causal=1, out=16, ots=2048, ohs=128, stream=None)
+                hq=16, hkv=8, d=128, scale=0.088, causal=1, out=16, ots=2048, ohs=128, ws=256, wsb=1 << 30,
+                stream=None)
     args.update(over)
     return _lib.lib().kvp_varlen_prefill_bf16(*args.values())
 
@@ -161,6 +162,23 @@ def test_prefill_rejects_bad_arguments_on_host():
     assert _prefill(vts=1 << 24) == _lib.KVP_EINVAL              # 64 rows beyond 32-bit offsets
     assert b"token strides" in _lib.lib().kvp_last_error()
     assert _prefill(cuq=None) == _lib.KVP_EINVAL
+    assert _prefill(wsb=100) == _lib.KVP_EWORKSPACE              # smaller than the work list
+    assert b"workspace" in _lib.lib().kvp_last_error()
+    assert _prefill(ws=None) == _lib.KVP_EWORKSPACE
+    assert _prefill(ws=64) == _lib.KVP_EINVAL                    # not 256-byte aligned
+
+
+def test_prefill_workspace_size_formula():
+    # 2 KiB (claim counters, unit count) plus 32 bytes per (sequence, pair of query tiles);
+    # a tile holds 128 / G query tokens; at most 2048 sequences per launch
+    size = _lib.lib().kvp_prefill_workspace_bytes
+    assert size(32, 1024, 16, 8) == 2048 + 32 * 32 * 8          # G = 2: 16 tiles, 8 pairs
+    assert size(256, 4096, 16, 8) == 2048 + 32 * 256 * 32
+    assert size(3, 100, 40, 8) == 2048 + 32 * 3 * 2             # G = 5: 25-token tiles, 4 tiles
+    assert size(5000, 1, 8, 1) == 2048 + 32 * 2048 * 1           # G = 8, capped at one launch
+    assert size(4, 0, 16, 8) == 2048
+    assert size(4, 100, 24, 8) == 0                              # GQA ratio 3
+    assert size(4, 100, 12, 8) == 0
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
