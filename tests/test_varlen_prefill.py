@@ -377,3 +377,63 @@ def test_rising_scores_rebase_the_running_max(cuda_device, paged):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     torch.testing.assert_close(out.cpu().float(), want, **TOL)
+
+
+def test_prefill_graph_replay_with_new_data(cuda_device):
+    """Prefill captured in a graph after reserving its workspace: each replay's plan kernel
+    rewrites the work list and zeroes the claim counters in the workspace (no memset is
+    recorded), so replays with new queries, keys and lengths written into the captured
+    buffers equal eager calls bit for bit.  Eager work runs between the replays."""
+    from kavor_amd.layers.attention import reserve_prefill_workspace, varlen_prefill
+
+    d = cuda_device
+    hq, hkv, bs, nb, nseq = 16, 8, 64, 96, 6
+    g = gen(280)
+    kc = randn_bf16((nb, bs, hkv, 128), g).to(d)
+    vc = randn_bf16((nb, bs, hkv, 128), g).to(d)
+    width = 16
+    q = torch.zeros(6 * 256, hq, 128, dtype=torch.bfloat16, device=d)
+    cq = torch.zeros(nseq + 1, dtype=torch.int32, device=d)
+    ck = torch.zeros(nseq + 1, dtype=torch.int32, device=d)
+    bt = torch.zeros(nseq, width, dtype=torch.int32, device=d)
+    out = torch.zeros_like(q)
+    max_q = 256
+    reserve_prefill_workspace(nseq, max_q, hq, hkv, d)
+
+    def draw(seed):
+        g2 = gen(seed)
+        qlens = [int(x) for x in torch.randint(1, max_q + 1, (nseq,), generator=g2)]
+        prefix = [64 * int(x) for x in torch.randint(0, 6, (nseq,), generator=g2)]
+        klens = [a + b for a, b in zip(qlens, prefix)]
+        tables = torch.randint(0, nb, (nseq, width), generator=g2, dtype=torch.int32)
+        return qlens, klens, tables, randn_bf16((sum(qlens), hq, 128), g2)
+
+    def load(qlens, klens, tables, qd):
+        q.zero_()
+        q[:qd.shape[0]] = qd.to(d)
+        cq.copy_(_cu(qlens))
+        ck.copy_(_cu(klens))
+        bt.copy_(tables)
+
+    def call():
+        return varlen_prefill(q, kc, vc, max_q, cq, 0, ck, SCALE, causal=True, block_table=bt, out=out)
+
+    load(*draw(281))
+    call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(3):
+        qlens, klens, tables, qd = draw(282 + rep)
+        load(qlens, klens, tables, qd)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out[:sum(qlens)].clone()
+        eager = varlen_prefill(q, kc, vc, max_q, cq, 0, ck, SCALE, causal=True, block_table=bt)[:sum(qlens)]
+        torch.cuda.synchronize()
+        assert bits_equal(got.cpu(), eager.cpu()), f"replay {rep}"
+        want = ref.varlen_prefill(qd, kc.cpu(), vc.cpu(), _cu(qlens), _cu(klens), SCALE, block_tables=tables)
+        torch.testing.assert_close(got.cpu().float(), want, **TOL)
