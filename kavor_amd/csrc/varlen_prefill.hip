@@ -640,21 +640,48 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();  // every wave is done with the tile buffers (the next unit restages them)
 
-    // ---- write O: lane holds dims 32mb + 8(j/4) + 4hf + (j%4) of its query row
-    if (row_valid) {
-      const bool poisoned = bad;
-      const float inv = poisoned ? NAN : (l_run > 0.f ? 1.f / l_run : 0.f);
-      uint16_t* op = p.out + static_cast<int64_t>(q_start + qi) * p.o_tok_stride +
-                     static_cast<int64_t>(kvh * G + g) * p.o_head_stride;
+    // ---- write O through LDS.  The lane holds dims 32mb + 8(j/4) + 4hf + (j%4) of its
+    // query row, so a direct store writes 16 bytes into each of 32 rows; staged in the
+    // finished tile buffers (each wave its own 32 rows, rewritten by the next query tile's
+    // second key tile only after that tile's barrier), every store instruction writes
+    // whole rows.  A row's 16-byte chunk c sits at chunk c ^ (row & 15) and its 8-byte
+    // halves swap for rows 16..31, so neither the 8-byte writes nor the 16-byte reads
+    // share a bank.  Dense 32-sequence prefill 92.9 -> 88.1 us, prefix-cached 343.0 ->
+    // 341.1 us, same outputs.
+    {
+      const float inv = bad ? NAN : (l_run > 0.f ? 1.f / l_run : 0.f);
+      uint16_t* const stg = (wave < 2 ? s_k1 : s_v1) + (wave & 1) * 32 * kPrefillHeadDim;
+      // lane index recomputed here: offsets derived from it are not hoisted out of the
+      // unit loop (where they would hold 24 registers through the key loop)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int nn = ln & 31, hh = ln >> 5;
+      const int hsw = (nn >> 4) & 1;
 #pragma unroll
       for (int mb = 0; mb < D / 32; ++mb)
 #pragma unroll
         for (int jq = 0; jq < 4; ++jq) {
-          const int d0 = 32 * mb + 8 * jq + 4 * hf;
+          const int c = 4 * mb + jq;
           const uint2 w = make_uint2(pack_bf16x2(oacc[mb][4 * jq] * inv, oacc[mb][4 * jq + 1] * inv),
                                      pack_bf16x2(oacc[mb][4 * jq + 2] * inv, oacc[mb][4 * jq + 3] * inv));
-          *reinterpret_cast<uint2*>(op + d0) = w;
+          *reinterpret_cast<uint2*>(stg + nn * kPrefillHeadDim + 8 * (c ^ (nn & 15)) + 4 * (hh ^ hsw)) = w;
         }
+      __builtin_amdgcn_wave_barrier();  // a wave's LDS accesses run in order
+      const int chunk = ln & 15;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = 4 * i + (ln >> 4);
+        uint4 v = *reinterpret_cast<const uint4*>(stg + row * kPrefillHeadDim + 8 * (chunk ^ (row & 15)));
+        if ((row >> 4) & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        const int rho_o = 32 * wave + row;
+        const int tq_o = rho_o / G;
+        const int qi_o = q0 + tq_o;
+        if (tq_o < TOK && qi_o < qlen) {
+          uint16_t* op = p.out + static_cast<int64_t>(q_start + qi_o) * p.o_tok_stride +
+                         static_cast<int64_t>(kvh * G + rho_o - tq_o * G) * p.o_head_stride + 8 * chunk;
+          *reinterpret_cast<uint4*>(op) = v;
+        }
+      }
     }
   }
   // The next claim is taken only now, when the workgroup is ready to start it: the two
@@ -770,11 +797,11 @@ extern "C" int kvp_varlen_prefill_bf16(const void* q, int64_t q_tok_stride, int6
   }
   if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out)
     return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: null pointer");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: q/k/v must be 16-byte and out 8-byte aligned");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: q/k/v/out must be 16-byte aligned");
   if (!mult8(q_tok_stride) || !mult8(q_head_stride) || !mult8(k_tok_stride) || !mult8(k_head_stride) ||
-      !mult8(v_tok_stride) || !mult8(v_head_stride) || (out_tok_stride & 3) || (out_head_stride & 3))
-    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: q/k/v strides must be multiples of 8, out of 4 elements");
+      !mult8(v_tok_stride) || !mult8(v_head_stride) || !mult8(out_tok_stride) || !mult8(out_head_stride))
+    return fail(KVP_EINVAL, "kvp_varlen_prefill_bf16: q/k/v/out strides must be multiples of 8 elements");
   // a K/V tile's 64 rows are addressed with 32-bit byte offsets
   if (k_tok_stride <= 0 || v_tok_stride <= 0 || k_tok_stride > INT32_MAX / (2 * kKeyTile) ||
       v_tok_stride > INT32_MAX / (2 * kKeyTile))

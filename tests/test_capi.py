@@ -166,6 +166,9 @@ def test_prefill_rejects_bad_arguments_on_host():
     assert b"workspace" in _lib.lib().kvp_last_error()
     assert _prefill(ws=None) == _lib.KVP_EWORKSPACE
     assert _prefill(ws=64) == _lib.KVP_EINVAL                    # not 256-byte aligned
+    assert _prefill(out=24) == _lib.KVP_EINVAL                   # out rows are stored 16 bytes at a time
+    assert _prefill(ots=2044) == _lib.KVP_EINVAL
+    assert b"out" in _lib.lib().kvp_last_error()
 
 
 def test_prefill_workspace_size_formula():
