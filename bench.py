@@ -25,6 +25,7 @@ decode tok/s (decode tokens / decode step time).
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import math
 import os
@@ -865,6 +866,7 @@ PROFILE_KERNELS = [
     ("paged_decode_qwen3_8b", "void kvp::paged_decode_kernel<4, 32, false>", "decode_8b"),
     ("kv_append_4096tok", "void kvp::kv_append_kernel<128", "append"),
     ("varlen_prefill_prefix_32seq", "void kvp::varlen_prefill_kernel<2, true, true>", "prefill"),
+    ("varlen_prefill_dense_32seq", "void kvp::varlen_prefill_kernel<2, false, true>", "prefill_dense"),
     ("qk_norm_rope_append_16384tok", "void kvp::(anonymous namespace)::qk_norm_rope_append_kernel<4>", "qk_norm_rope_append"),
     ("add_rmsnorm_16384x1024", "void kvp::(anonymous namespace)::rmsnorm_kernel<64, 2>", "add_rmsnorm"),
     ("silu_mul_16384x3072", "kvp::(anonymous namespace)::silu_mul_kernel", "silu_mul"),
@@ -905,8 +907,15 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         "decode_fused_0.6b": _decode_algo_bytes(256, 16, 100, 2048, 4096, fused=True),
         "decode_8b": _decode_algo_bytes(128, 32, 1024, 32768, 20000),
         "append": 32522240,
-        "prefill": 352688504832,
     }
+    # prefill: flops, and the algorithmic bytes beside them (prefill_bytes)
+    qlens, klens, tables = prefill_workload()
+    cq = [0] + list(itertools.accumulate(qlens))
+    prefill_bytes_of = {}
+    for key, kls, tbl in (("prefill", klens, tables), ("prefill_dense", qlens, None)):
+        ck = [0] + list(itertools.accumulate(kls))
+        algo[key] = prefill_flops(cq, ck, 16, D)
+        prefill_bytes_of[key] = prefill_bytes(cq, ck, 16, 8, D, tbl, BS)
     algo.update(layer_algo_bytes(dict(T=LAYER_TOKENS, hq=16, hkv=8, H=1024, I=3072)))
     out_dir = ROOT / "profiles"
     out_dir.mkdir(exist_ok=True)
@@ -929,10 +938,15 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
         lines += [f"- dispatches: {len(all_us)}; over the last {len(d_us)} (after the warm-up launches) "
                   f"duration avg {avg_us:.2f} us, median {med_us:.2f} us, min {min(d_us):.2f}, "
                   f"max {max(d_us):.2f}"]
-        if key == "prefill":
+        if key.startswith("prefill"):
+            nb = prefill_bytes_of[key]
             lines += [f"- algorithmic work: {algo[key]} flop (unmasked query-key pairs x 4 x Hq x D) "
                       f"-> {algo[key] / med_us / 1e6:.1f} TFLOP/s at the median duration "
-                      f"({algo[key] / med_us / 1e6 / BF16_PEAK_TFLOPS * 100:.1f}% of 2.5 PFLOP/s dense bf16)"]
+                      f"({algo[key] / med_us / 1e6 / BF16_PEAK_TFLOPS * 100:.1f}% of 2.5 PFLOP/s dense bf16)",
+                      f"- algorithmic bytes: {nb} (q and o once, each distinct key's K and V once) -> "
+                      f"{nb / med_us / 1e3:.1f} GB/s at the median duration "
+                      f"({nb / med_us / 1e3 / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s); intensity "
+                      f"{algo[key] / nb:.0f} flop/B against the ridge point of 312 flop/B"]
         else:
             lines += [f"- algorithmic bytes: {algo[key]} -> {algo[key] / med_us / 1e3:.1f} GB/s at the median "
                       f"duration ({algo[key] / med_us / 1e3 / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)"]
@@ -943,7 +957,8 @@ def summarize_profiles(trace_dir: str, fetch_dir: str, write_dir: str) -> int:
                   f"WRITE_SIZE: 1 GiB copy writes {copy_w:.1f} KiB -> scale {w_scale:.4f}",
                   f"- HBM traffic per dispatch (scaled): read {statistics.mean(fetch):.0f} B, "
                   f"write {statistics.mean(write):.0f} B, total {traffic:.0f} B"
-                  + (f" = {traffic / algo[key]:.4f} x algorithmic" if key != "prefill" else "")]
+                  + (f" = {traffic / (prefill_bytes_of[key] if key.startswith('prefill') else algo[key]):.4f} "
+                     f"x algorithmic")]
         if key.startswith("decode") and merge_name in dur:
             m_us = [x / 1e3 for x in dur[merge_name]]
             m_us = m_us[len(m_us) // 3:]

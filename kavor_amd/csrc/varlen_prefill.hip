@@ -24,10 +24,11 @@
 //   softmax scale is folded into the exponent (exp2(fma(s, scale*log2 e, -m))).
 //   Q stays in registers for the whole key loop (8 x 16 bytes per lane).
 //   Work order: a one-workgroup plan kernel ranks the units of work (a pair of
-//   neighbouring query tiles of one sequence and kv head) by cost into a caller
-//   workspace; persistent workgroups (two per CU) then claim them in that order from
-//   per-XCD counters, so the most expensive units start first, the cheap ones fill in
-//   behind them, and the two tiles of a unit run on one XCD.
+//   neighbouring query tiles of one sequence and kv head) sequence by sequence, longest
+//   sequence first, into a caller workspace; persistent workgroups (two per CU) then
+//   claim them in that order from per-XCD counters, so the most expensive sequences start
+//   first, a sequence's query tiles run together and stream its K/V through one XCD's L2,
+//   and the cheap ones fill in behind them.
 #include <math.h>
 
 #include <algorithm>
@@ -85,16 +86,21 @@ struct PrefillParams {
   int* ws;  // launch workspace: claim counters, unit count, ranked unit pairs
 };
 
-// Ranks the launch's units by cost for the persistent attention workgroups.  A unit is a
-// pair of neighbouring query tiles of one (sequence, kv head); its cost is the key-tile
-// count of its later (longer) tile, ceil(min(kl, min(ql, (i + 1) TOK) + kl - ql) / 64)
-// for tile i (kl without the causal mask), and unit j of a sequence with ntl query tiles
-// starts at tile ntl - 1 - 2j (j < J; J = pair_slots covers max_seqlen_q).  One workgroup
-// histograms the (sequence, j) pairs by cost, turns the histogram into offsets in
-// decreasing cost and places each pair; every kv head of a pair follows it in rank order.
-// It also zeroes the claim counters, so a workspace needs no clearing.  Pairs of one cost
-// are placed in no fixed order: the attention outputs do not depend on the order.
-template <int G, bool CAUSAL>
+// Ranks the launch's units for the persistent attention workgroups.  A unit is a pair of
+// neighbouring query tiles of one (sequence, kv head); unit j of a sequence with ntl query
+// tiles starts at tile ntl - 1 - 2j (j < J; J = pair_slots covers max_seqlen_q).  Every
+// unit of a sequence ranks at the sequence's key-tile count ceil(kl / 64), the cost of its
+// last query tile and an upper bound on the cost of any of its tiles: the longest
+// sequences go first, and a sequence's units are claimed together, so its query tiles read
+// each K/V tile at about the same time and share it through one XCD's L2.  (Ranking each
+// unit at its own cost spread a sequence's tiles over the whole call: on the
+// prefix-cached 32-sequence workload 390 MB were read per call against 319 MB, on its dense
+// form 320 MB against 164 MB, at equal or longer times.)  One workgroup histograms the
+// (sequence, j) pairs by level, turns the histogram into offsets in decreasing level and
+// places each pair; every kv head of a pair follows it in rank order.  It also zeroes the
+// claim counters, so a workspace needs no clearing.  Pairs of one level are placed in no
+// fixed order: the attention outputs do not depend on the order.
+template <int G>
 __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const PrefillParams p) {
   constexpr int TOK = kPrefillRows / G;
   __shared__ int hist[kPlanLevels];
@@ -106,11 +112,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const Prefil
   if (tid == 0) total = 0;
   __syncthreads();
   const int J = p.pair_slots;
-  auto level = [&](int ql, int kl, int j) {
-    const int i = (ql + TOK - 1) / TOK - 1 - kXcdGroup * j;
-    const int e = CAUSAL ? min(kl, min(ql, (i + 1) * TOK) + kl - ql) : kl;
-    return min(max((e + kKeyTile - 1) / kKeyTile, 0), kPlanLevels - 1);
-  };
+  auto level = [&](int kl) { return min(max((kl + kKeyTile - 1) / kKeyTile, 0), kPlanLevels - 1); };
   int q0[kPlanSeqsPerThread], ql[kPlanSeqsPerThread], k0[kPlanSeqsPerThread], kl[kPlanSeqsPerThread];
   int mine = 0;
 #pragma unroll
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const Prefil
       kl[u] = p.cu_k[sq + 1] - k0[u];
     }
     const int nu = min(J, ((ql[u] + TOK - 1) / TOK + kXcdGroup - 1) / kXcdGroup);
-    for (int j = 0; j < nu; ++j) atomicAdd(&hist[level(ql[u], kl[u], j)], 1);
+    if (nu) atomicAdd(&hist[level(kl[u])], nu);
     mine += nu;
   }
   if (mine) atomicAdd(&total, mine);
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const Prefil
     const int sq = tid + kPlanThreads * u;
     const int nu = min(J, ((ql[u] + TOK - 1) / TOK + kXcdGroup - 1) / kXcdGroup);
     for (int j = 0; j < nu; ++j) {
-      const int pos = atomicAdd(&hist[level(ql[u], kl[u], j)], 1);
+      const int pos = atomicAdd(&hist[level(kl[u])], 1);
       *reinterpret_cast<int4*>(units + kUnitInts * pos) = make_int4(sq, j, q0[u], ql[u]);
       *reinterpret_cast<int4*>(units + kUnitInts * pos + 4) = make_int4(k0[u], kl[u], 0, 0);
     }
@@ -200,11 +202,11 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   constexpr int D = kPrefillHeadDim;
   constexpr int TOK = kPrefillRows / G;  // query tokens per tile
 
-  // Work order.  The plan kernel listed the units in decreasing cost; persistent
-  // workgroups claim them in that order, so the most expensive units start first and the
-  // cheap ones fill in behind them (0.82 -> 0.58 ms for "last tiles first" against
-  // (sequence, kv head, tile) order, then 0.457 -> 0.437 ms for the global cost order,
-  // one workgroup per unit).  Claims come from one counter per XCD: workgroup b runs on
+  // Work order.  The plan kernel listed the units sequence by sequence, longest first;
+  // persistent workgroups claim them in that order, so the most expensive work starts
+  // first and the cheap work fills in behind it (0.82 -> 0.58 ms for "last tiles first"
+  // against (sequence, kv head, tile) order, then 0.457 -> 0.437 ms for a global cost
+  // order, one workgroup per unit).  Claims come from one counter per XCD: workgroup b runs on
   // XCD b % 8 (the hardware deals workgroup ids round-robin to the 8 XCDs), claim c of
   // XCD x is rank 8 (c / 2) + x, and its two tiles go to two consecutive claims, so both
   // tiles of a unit, which read nearly the same K/V, run together on one XCD and share its
@@ -723,7 +725,7 @@ static int64_t prefill_resident() {
 // persistent workgroups (a multiple of 16, so each XCD holds the same number) claims them.
 template <int G, bool PAGED, bool CAUSAL>
 static void launch_variant(hipStream_t s, const PrefillParams& p) {
-  hipLaunchKernelGGL((prefill_plan_kernel<G, CAUSAL>), dim3(1), dim3(kPlanThreads), 0, s, p);
+  hipLaunchKernelGGL((prefill_plan_kernel<G>), dim3(1), dim3(kPlanThreads), 0, s, p);
   const int64_t grid = prefill_resident<G, PAGED, CAUSAL>();
   hipLaunchKernelGGL((varlen_prefill_kernel<G, PAGED, CAUSAL>), dim3(static_cast<unsigned>(grid)),
                      dim3(kPrefillThreads), 0, s, p);

@@ -1,10 +1,10 @@
 """The prefill's work order (varlen_prefill.hip): a Python mirror of the plan kernel
 (prefill_plan_kernel) and of the persistent workgroups' claims, checked on the CPU.
 
-The plan kernel histograms the (sequence, pair index j) pairs by the key-tile count of
-the pair's later tile, turns the histogram into offsets in decreasing cost, and places
-each pair at the next offset of its level (LDS atomics: pairs of one level land in no
-fixed order).  Rank r is kv head r % H of pair r // H.  The workgroups of XCD x claim
+The plan kernel histograms the (sequence, pair index j) pairs by their sequence's
+key-tile count ceil(kl / 64), turns the histogram into offsets in decreasing level, and
+places each pair at the next offset of its level (LDS atomics: pairs of one level land
+in no fixed order).  Rank r is kv head r % H of pair r // H.  The workgroups of XCD x claim
 c = 0, 1, 2, ... from their own counter; claim c is rank 8 (c // 2) + x, member c % 2 (the
 earlier tile of the pair), and a member takes query tiles t = 2j + member, t + 2J, ...
 counted from the sequence's last tile.  The properties that keep the kernel correct and
@@ -13,8 +13,10 @@ fast:
 - claims -> (sequence, kv head, query tile) cover every query tile exactly once, whatever
   order the pairs of one level land in, also when max_seqlen_q understates the longest
   sequence (units then stride over tile pairs) and when a pair has no earlier tile;
-- the cost by rank never increases;
-- a pair's level is the key-tile count the kernel's key loop runs for its later tile.
+- the level by rank never increases, and every pair of a sequence has the same level;
+- a pair's level bounds the key-tile count the kernel's key loop runs for its later
+  tile, and equals it for the sequence's last pair (the longest tile), so the longest
+  sequences start first.
 
 The GPU tests check the kernel's outputs against the oracle on the same shapes."""
 
@@ -34,16 +36,14 @@ def tile_cost(ql, kl, i, tok, causal):
 def plan(lens, tok, causal, pair_slots, rng):
     """The plan kernel: pairs (s, j) in decreasing level, ties shuffled (placement order
     within a level is whatever the LDS atomics give)."""
-    def level(ql, kl, j):
-        i = (ql + tok - 1) // tok - 1 - 2 * j
-        e = min(kl, min(ql, (i + 1) * tok) + kl - ql) if causal else kl
-        return min(max(-(-e // KEY_TILE) if e > 0 else 0, 0), PLAN_LEVELS - 1)
+    def level(kl):
+        return min(max(-(-kl // KEY_TILE), 0), PLAN_LEVELS - 1)
 
     by_level = {}
     for s, (ql, kl) in enumerate(lens):
         nu = min(pair_slots, ((ql + tok - 1) // tok + 1) // 2)
         for j in range(nu):
-            by_level.setdefault(level(ql, kl, j), []).append((s, j))
+            by_level.setdefault(level(kl), []).append((s, j))
     pairs = []
     for lv in sorted(by_level, reverse=True):
         group = by_level[lv]
@@ -59,6 +59,9 @@ def check_order(lens, heads, group, causal, max_seqlen_q, rng):
     num_units = len(pairs) * heads
     levels = [pairs[r // heads][2] for r in range(num_units)]
     assert all(a >= b for a, b in zip(levels, levels[1:]))
+    seq_level = {}
+    for s, _, lv in pairs:
+        assert seq_level.setdefault(s, lv) == lv
     seen = set()
     for xcd in range(8):
         c = 0
@@ -72,7 +75,8 @@ def check_order(lens, heads, group, causal, max_seqlen_q, rng):
             q, k = lens[s]
             ntl = (q + tok - 1) // tok
             assert 0 <= j < pair_slots
-            assert min(tile_cost(q, k, ntl - 1 - 2 * j, tok, causal), PLAN_LEVELS - 1) == lv
+            cost = min(tile_cost(q, k, ntl - 1 - 2 * j, tok, causal), PLAN_LEVELS - 1)
+            assert cost <= lv and (j > 0 or cost == lv), (q, k, j, cost, lv)
             t = 2 * j + member
             while t < ntl:  # a member past the last tile has no query tile (an empty unit)
                 key = (s, kvh, ntl - 1 - t)
