@@ -56,6 +56,7 @@ constexpr int kUnitInts = 8;               // s, pair index, q start, q length, 
 constexpr int kPlanThreads = 256;
 constexpr int kPlanSeqsPerThread = kMaxPrefillSeqs / kPlanThreads;
 constexpr int kPlanLevels = 2048;          // cost levels (64-key tiles) ranked apart; longer units tie at the top
+constexpr int kPlanGroupSlots = 4096;      // first-block hash slots, more than kMaxPrefillSeqs: a probe always ends
 static_assert(kPlanLevels % kPlanThreads == 0 && kMaxPrefillSeqs % kPlanThreads == 0, "plan shape");
 // A tile's row sum of P above this re-bases the running max (P itself stays <= 2^16).
 constexpr float kSpecSumLimit = 65536.f;
@@ -100,36 +101,74 @@ struct PrefillParams {
 // places each pair; every kv head of a pair follows it in rank order.  It also zeroes the
 // claim counters, so a workspace needs no clearing.  Pairs of one level are placed in no
 // fixed order: the attention outputs do not depend on the order.
+// With block tables, sequences that start with the same cache block (a prefix-cache hit:
+// their leading pages are shared) rank together at the level of the longest of them, so
+// they run at the same time and the shared prefix passes through each XCD's L2 once for
+// the group rather than once per sequence.  An LDS hash table keyed by the first block id
+// holds each group's largest level.
 template <int G>
 __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const PrefillParams p) {
   constexpr int TOK = kPrefillRows / G;
   __shared__ int hist[kPlanLevels];
   __shared__ int wsum[kPlanThreads / 64];
   __shared__ int total;
+  __shared__ int grp_key[kPlanGroupSlots];  // first block id, -1 for an empty slot
+  __shared__ int grp_lvl[kPlanGroupSlots];  // the largest level of the sequences starting with it
   const int tid = threadIdx.x;
+  const bool grouped = p.block_tables != nullptr && p.max_blocks > 0;
   for (int i = tid; i < kPlanLevels; i += kPlanThreads) hist[i] = 0;
+  if (grouped) {
+    for (int i = tid; i < kPlanGroupSlots; i += kPlanThreads) {
+      grp_key[i] = -1;
+      grp_lvl[i] = 0;
+    }
+  }
   if (tid < 8) p.ws[kClaimStride * tid] = 0;
   if (tid == 0) total = 0;
   __syncthreads();
   const int J = p.pair_slots;
   auto level = [&](int kl) { return min(max((kl + kKeyTile - 1) / kKeyTile, 0), kPlanLevels - 1); };
+  // the hash slot of a first block id, inserted if absent (linear probing; fewer ids than
+  // slots, so a free or matching slot is always found)
+  auto group_slot = [&](int key) {
+    int h = static_cast<int>((static_cast<uint32_t>(key) * 2654435769u) >> 20) & (kPlanGroupSlots - 1);
+    for (int probe = 0; probe < kPlanGroupSlots; ++probe) {
+      const int prev = atomicCAS(&grp_key[h], -1, key);
+      if (prev == -1 || prev == key) return h;
+      h = (h + 1) & (kPlanGroupSlots - 1);
+    }
+    return -1;
+  };
   int q0[kPlanSeqsPerThread], ql[kPlanSeqsPerThread], k0[kPlanSeqsPerThread], kl[kPlanSeqsPerThread];
+  int gs[kPlanSeqsPerThread];  // group slot, -1 for a sequence ranked alone
   int mine = 0;
 #pragma unroll
   for (int u = 0; u < kPlanSeqsPerThread; ++u) {
     const int sq = tid + kPlanThreads * u;
     q0[u] = ql[u] = k0[u] = kl[u] = 0;
+    gs[u] = -1;
     if (sq < p.num_seqs) {
       q0[u] = p.cu_q[sq];
       ql[u] = p.cu_q[sq + 1] - q0[u];
       k0[u] = p.cu_k[sq];
       kl[u] = p.cu_k[sq + 1] - k0[u];
+      const int b0 = grouped && kl[u] > 0 && ql[u] > 0 ? p.block_tables[sq * p.bt_stride] : -1;
+      if (b0 >= 0) {
+        gs[u] = group_slot(b0);
+        if (gs[u] >= 0) atomicMax(&grp_lvl[gs[u]], level(kl[u]));
+      }
     }
-    const int nu = min(J, ((ql[u] + TOK - 1) / TOK + kXcdGroup - 1) / kXcdGroup);
-    if (nu) atomicAdd(&hist[level(kl[u])], nu);
-    mine += nu;
+    mine += min(J, ((ql[u] + TOK - 1) / TOK + kXcdGroup - 1) / kXcdGroup);
   }
   if (mine) atomicAdd(&total, mine);
+  __syncthreads();
+  int lv[kPlanSeqsPerThread];
+#pragma unroll
+  for (int u = 0; u < kPlanSeqsPerThread; ++u) {
+    lv[u] = gs[u] >= 0 ? grp_lvl[gs[u]] : level(kl[u]);
+    const int nu = min(J, ((ql[u] + TOK - 1) / TOK + kXcdGroup - 1) / kXcdGroup);
+    if (nu) atomicAdd(&hist[lv[u]], nu);
+  }
   __syncthreads();
   // exclusive offsets in decreasing cost: thread t owns the kPlanLevels / kPlanThreads
   // levels just below the ones of thread t - 1
@@ -158,7 +197,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const Prefil
     const int sq = tid + kPlanThreads * u;
     const int nu = min(J, ((ql[u] + TOK - 1) / TOK + kXcdGroup - 1) / kXcdGroup);
     for (int j = 0; j < nu; ++j) {
-      const int pos = atomicAdd(&hist[level(kl[u])], 1);
+      const int pos = atomicAdd(&hist[lv[u]], 1);
       *reinterpret_cast<int4*>(units + kUnitInts * pos) = make_int4(sq, j, q0[u], ql[u]);
       *reinterpret_cast<int4*>(units + kUnitInts * pos + 4) = make_int4(k0[u], kl[u], 0, 0);
     }
