@@ -116,6 +116,24 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const Prefil
   __shared__ int grp_lvl[kPlanGroupSlots];  // the largest level of the sequences starting with it
   const int tid = threadIdx.x;
   const bool grouped = p.block_tables != nullptr && p.max_blocks > 0;
+  // The launch's lengths and first block ids, loaded before the LDS is initialised so
+  // that their round trip overlaps it.  Every sequence has a block-table row with at
+  // least one entry, so the first entry is read whatever the lengths.
+  int q0[kPlanSeqsPerThread], ql[kPlanSeqsPerThread], k0[kPlanSeqsPerThread], kl[kPlanSeqsPerThread];
+  int b0[kPlanSeqsPerThread];
+#pragma unroll
+  for (int u = 0; u < kPlanSeqsPerThread; ++u) {
+    const int sq = tid + kPlanThreads * u;
+    q0[u] = ql[u] = k0[u] = kl[u] = 0;
+    b0[u] = -1;
+    if (sq < p.num_seqs) {
+      q0[u] = p.cu_q[sq];
+      ql[u] = p.cu_q[sq + 1];
+      k0[u] = p.cu_k[sq];
+      kl[u] = p.cu_k[sq + 1];
+      if (grouped) b0[u] = p.block_tables[sq * p.bt_stride];
+    }
+  }
   for (int i = tid; i < kPlanLevels; i += kPlanThreads) hist[i] = 0;
   if (grouped) {
     for (int i = tid; i < kPlanGroupSlots; i += kPlanThreads) {
@@ -139,24 +157,16 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const Prefil
     }
     return -1;
   };
-  int q0[kPlanSeqsPerThread], ql[kPlanSeqsPerThread], k0[kPlanSeqsPerThread], kl[kPlanSeqsPerThread];
   int gs[kPlanSeqsPerThread];  // group slot, -1 for a sequence ranked alone
   int mine = 0;
 #pragma unroll
   for (int u = 0; u < kPlanSeqsPerThread; ++u) {
-    const int sq = tid + kPlanThreads * u;
-    q0[u] = ql[u] = k0[u] = kl[u] = 0;
+    ql[u] -= q0[u];
+    kl[u] -= k0[u];
     gs[u] = -1;
-    if (sq < p.num_seqs) {
-      q0[u] = p.cu_q[sq];
-      ql[u] = p.cu_q[sq + 1] - q0[u];
-      k0[u] = p.cu_k[sq];
-      kl[u] = p.cu_k[sq + 1] - k0[u];
-      const int b0 = grouped && kl[u] > 0 && ql[u] > 0 ? p.block_tables[sq * p.bt_stride] : -1;
-      if (b0 >= 0) {
-        gs[u] = group_slot(b0);
-        if (gs[u] >= 0) atomicMax(&grp_lvl[gs[u]], level(kl[u]));
-      }
+    if (b0[u] >= 0 && kl[u] > 0 && ql[u] > 0) {
+      gs[u] = group_slot(b0[u]);
+      if (gs[u] >= 0) atomicMax(&grp_lvl[gs[u]], level(kl[u]));
     }
     mine += min(J, ((ql[u] + TOK - 1) / TOK + kXcdGroup - 1) / kXcdGroup);
   }
