@@ -199,6 +199,10 @@ int kvp_paged_decode_bf16_noalloc(const void* q, int64_t q_seq_stride, int64_t q
  *                         outside [0, num_cache_blocks) or klen_s larger than
  *                         max_blocks_per_seq * block_size makes that sequence's
  *                         output NaN.  block_size must be a multiple of 64.
+ *                         Every sequence has a row (block_table_stride apart) of
+ *                         max_blocks_per_seq >= 1 entries; the first entry of each
+ *                         row is read even for a sequence without queries (sequences
+ *                         that start with the same block are scheduled together).
  * q, k, v and out are 16-byte aligned, head_dim is contiguous and every other stride is a
  * multiple of 8 elements (KVP_EINVAL otherwise).
  * max_seqlen_q only sizes the work list: a sequence longer than it is still computed in
