@@ -100,12 +100,16 @@ struct PrefillParams {
 // (sequence, j) pairs by level, turns the histogram into offsets in decreasing level and
 // places each pair; every kv head of a pair follows it in rank order.  It also zeroes the
 // claim counters, so a workspace needs no clearing.  Pairs of one level are placed in no
-// fixed order: the attention outputs do not depend on the order.
+// fixed order (the attention outputs do not depend on it), but the LDS atomics interleave
+// the level's sequences pair index by pair index, so every sequence's longest pair is
+// claimed before the shorter ones of its level (placing each sequence's pairs together
+// read 250 MB instead of 279 MB but ran 1.7% slower).
 // With block tables, sequences that start with the same cache block (a prefix-cache hit:
 // their leading pages are shared) rank together at the level of the longest of them, so
 // they run at the same time and the shared prefix passes through each XCD's L2 once for
-// the group rather than once per sequence.  An LDS hash table keyed by the first block id
-// holds each group's largest level.
+// the group rather than once per sequence (316 -> 278 MB per call on the prefix-cached
+// workload, same time).  An LDS hash table keyed by the first block id holds each group's
+// largest level.
 template <int G>
 __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const PrefillParams p) {
   constexpr int TOK = kPrefillRows / G;
