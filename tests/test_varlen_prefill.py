@@ -309,9 +309,10 @@ def test_paged_relocated_pages_are_bitwise_identical(cuda_device):
 
 @pytest.mark.parametrize("paged", [True, False])
 def test_more_sequences_than_one_launch(cuda_device, paged):
-    """4100 sequences run as several launches (paged: 2048 + 2048 + 4; dense: 4 x 1024 +
-    4): the later ones read their cu_seqlens and block-table rows through offset pointers
-    and write the same absolute rows."""
+    """4100 sequences run as three launches (2048 + 2048 + 4): the later ones read their
+    cu_seqlens and block-table rows through offset pointers and write the same absolute
+    rows.  Paged, the random tables make sequences share first blocks, so the plan ranks
+    groups of up to dozens of sequences together."""
     g = gen(260 + paged)
     nseq, bs, nb = 4100, 64, 64
     qlens = [int(x) for x in torch.randint(1, 4, (nseq,), generator=g)]
