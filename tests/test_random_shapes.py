@@ -76,6 +76,14 @@ def test_random_prefill(cuda_device, seed):
         nb = sum(math.ceil(k / bs) for k in klens) + 2
         kc, vc = _pool(g, nb, bs, hkv, layout)
         bt = random_block_tables(klens, bs, nb, g)
+        if bool(torch.randint(0, 2, (1,), generator=g)):
+            # prefix-cache hits: some sequences start with the full leading pages of an
+            # earlier one (the plan ranks sequences that share a first block together)
+            for s2 in range(1, nseq):
+                s1 = int(torch.randint(0, s2 + 1, (1,), generator=g))
+                m = min(prefix[s1], prefix[s2]) // bs
+                if s1 != s2 and m:
+                    bt[s2, :m] = bt[s1, :m]
         out = varlen_prefill(q.to(d), kc.to(d), vc.to(d), max_seqlen_q=max_q, cu_seqlens_q=cq.to(d),
                              max_seqlen_k=max(klens), cu_seqlens_k=ck.to(d), softmax_scale=D ** -0.5,
                              causal=causal, block_table=bt.to(d))
